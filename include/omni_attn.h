@@ -1,0 +1,157 @@
+/*
+ * omni_attn — MI355X (gfx950) attention for the pega-omni engines, C ABI.
+ *
+ * Three kernels behind plan/run calls:
+ *   - paged GQA / MHA decode (split-K, bandwidth-bound, no MFMA),
+ *   - ragged causal chunked prefill over the same paged cache (bf16 MFMA),
+ *   - HiDream-O1 DiT attention over dense K/V caches, causal or full (bf16 MFMA).
+ *
+ * Conventions for every entry point:
+ *   - returns OMNI_ATTN_OK (0) or a negative OMNI_ATTN_E* code; nothing throws;
+ *   - device pointers are plain `void*` / `int32_t*`; bf16 data is passed as
+ *     `void*` (2-byte elements, head_dim 128);
+ *   - `*_run` calls launch on `stream` (a hipStream_t, passed as void*), never
+ *     allocate, never synchronise the host, and are safe to capture in a HIP
+ *     graph: lengths are read from device arrays at run time;
+ *   - `*_plan` calls are pure host code: they validate shapes and size the
+ *     workspace; the caller owns and allocates the workspace.
+ *
+ * Layouts are the reference's (paths in the pega-omni tree):
+ *   qkv row n: [(hq + 2 hk)][128] bf16, q heads first (qwen3.cu:5-7, lm.cu:285);
+ *   paged KV slot: [K heads | V heads][128] bf16 = 2 * hk * 256 bytes;
+ *   token t of sequence s lives in slot pages[indptr[s] + t / page] * page + t % page
+ *   (qwen3.cu:210-214); a row of sequence s at position pos sees tokens 0..pos;
+ *   out row n: [hq][128] bf16.
+ */
+#ifndef OMNI_ATTN_H
+#define OMNI_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OMNI_ATTN_OK 0
+#define OMNI_ATTN_EINVAL (-1)       /* bad argument (null pointer, negative size) */
+#define OMNI_ATTN_EUNSUPPORTED (-2) /* shape the kernels do not implement */
+#define OMNI_ATTN_ELAUNCH (-3)      /* the HIP launch failed */
+#define OMNI_ATTN_EWORKSPACE (-4)   /* workspace missing or too small */
+#define OMNI_ATTN_ETABLE (-5)       /* page table / indptr failed host validation */
+
+#define OMNI_ATTN_HEAD_DIM 128
+
+/* ------------------------------------------------------------------ decode */
+
+/* How a decode run partitions keys. Depends only on (rows, heads, page,
+ * max_len), never on the lengths of one step, so one plan serves every replay
+ * of a captured graph of the same batch bucket. */
+typedef struct omni_attn_decode_plan {
+  int32_t rows;     /* rows per launch (the batch bucket) */
+  int32_t hq, hk;   /* query heads, K/V heads (hq % hk == 0, hq / hk in {1,2,4,8}) */
+  int32_t page;     /* tokens per page, a power of two */
+  int32_t max_len;  /* bound on keys any row sees; longer rows still run, slower */
+  int32_t chunk;    /* keys per split (a multiple of 128) */
+  int32_t splits;   /* ceil(max_len / chunk): workgroups per (row, kv head) */
+  int32_t reserved;
+  int64_t workspace_bytes; /* device scratch `*_run` needs (split partials) */
+} omni_attn_decode_plan;
+
+/* Fill `plan`. chunk_hint <= 0 picks the split size from the shape. */
+int omni_attn_decode_plan_init(int rows, int hq, int hk, int page, int max_len, int chunk_hint,
+                               omni_attn_decode_plan* plan);
+
+/* Replaces `qwen3_attend` (crates/omni-qwen3/kernels/qwen3.cu:234-240): row n
+ * of sequence s = ragged ? seq[n] : n attends to pos[n] + 1 keys. Arguments in
+ * the reference's order, then the plan's rows, workspace and stream.
+ * `seq` may be NULL when ragged == 0. */
+int omni_qwen3_attend(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                      const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
+                      const omni_attn_decode_plan* plan, void* workspace, void* stream);
+
+/* Replaces `lm_attend` (crates/omni-personaplex/kernels/lm.cu:275-290) over
+ * bf16 slots: MHA with `heads` query and K/V heads, qkv rows [3 heads][128],
+ * each row sees min(pos[n] + 1, context) ring slots through its page table. */
+int omni_lm_attend(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                   const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
+                   int context, const omni_attn_decode_plan* plan, void* workspace, void* stream);
+
+/* Same kernels with the FlashInfer-style length encoding the engines can also
+ * produce: sequence s holds (indptr[s+1] - indptr[s] - 1) * page +
+ * last_page_len[s] tokens, and row n (sequence ragged ? seq[n] : n) sees all
+ * of them. qkv rows are [(hq + 2 hk)][128]. */
+int omni_attn_decode_run_lastlen(const void* qkv, const void* kv, const int32_t* last_page_len, const int32_t* seq,
+                                 int ragged, const int32_t* indptr, const int32_t* pages, int page, void* out, int hq,
+                                 int hk, float scale, const omni_attn_decode_plan* plan, void* workspace,
+                                 void* stream);
+
+/* ---------------------------------------------------------- page tables */
+
+/* Host check of a page table before upload: indptr monotone from 0, every
+ * page id in [0, num_pages), and every row's pos + 1 covered by its pages
+ * (min(pos + 1, context) when context > 0). The manifest-domain checks of
+ * crates/omni-qwen3-tts/src/model.rs:348-359, done once on the host. */
+int omni_attn_check_table(const int32_t* indptr_h, int nseqs, const int32_t* pages_h, int num_pages,
+                          const int32_t* pos_h, const int32_t* seq_h, int ragged, int rows, int page, int context);
+
+/* Bit-exact gather of paged K/V to dense rows: for i < nseq and t < lens[i],
+ * out[(out_indptr[i] + t)] = slot(seq_ids[i], t) of kv, 2 * hk * 128 bf16 each.
+ * The paged addressing every kernel uses, exposed for verification. */
+int omni_attn_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int page,
+                        const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
+                        void* stream);
+
+/* ------------------------------------------------------- prefill (MFMA) */
+
+/* Work list for a ragged causal prefill: rows of one sequence are contiguous
+ * and at consecutive positions (how Rows::push_seq lays them out,
+ * crates/omni-qwen3-tts/src/model.rs:278-289). */
+typedef struct omni_attn_prefill_plan {
+  int32_t rows, hq, hk, page;
+  int32_t tiles;     /* query tiles in the work list */
+  int32_t tile_rows; /* packed (position, head) rows per tile */
+  int64_t work_bytes; /* bytes of the int32 work list the caller uploads */
+} omni_attn_prefill_plan;
+
+/* Host: validate (seq_h, pos_h) for `rows` ragged rows and write the work list
+ * (4 int32 per tile) into work_h (capacity work_cap int32). Returns
+ * OMNI_ATTN_EWORKSPACE with plan->work_bytes set when work_h is too small. */
+int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_t* seq_h, const int32_t* pos_h,
+                                int32_t* work_h, int64_t work_cap, omni_attn_prefill_plan* plan);
+
+/* Ragged causal prefill with the semantics of qwen3_attend(ragged = 1): row n
+ * sees keys 0..pos[n] of sequence seq[n] through the page table. `work` is
+ * the device copy of the plan's work list. */
+int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, const void* kv, const int32_t* pos,
+                          const int32_t* seq, const int32_t* indptr, const int32_t* pages, void* out, float scale,
+                          const int32_t* work, void* stream);
+
+/* ---------------------------------------------------------- DiT (MFMA) */
+
+/* Replaces `hidream_attend` (crates/omni-hidream-o1/kernels/hidream.cu:209-347).
+ * q rows at q + n * q_stride + h * 128 (h < hq = G * hk), k and v [slots][hk][128],
+ * out [q_len][hq][128]; row n sees the first *kv_len_at keys, with causal
+ * only keys 0..n. The reference fixes G = 4 and hk = gridDim.y; here hq and hk
+ * are arguments (G in {1,2,4,8}). */
+int omni_hidream_attend(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
+                        int q_stride, int causal, float scale_log2, int hq, int hk, void* stream);
+
+/* Batched form: `batch` independent problems (the CFG pair) at element strides
+ * q_bstride, kv_bstride (k and v), out_bstride, sharing *kv_len_at. */
+int omni_hidream_attend_batched(const void* q, const void* k, const void* v, void* out, int q_len,
+                                const int32_t* kv_len_at, int q_stride, int causal, float scale_log2, int hq, int hk,
+                                int batch, int64_t q_bstride, int64_t kv_bstride, int64_t out_bstride, void* stream);
+
+/* ------------------------------------------------------------- library */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int omni_attn_version(void);
+
+/* Text of the last error raised on this thread by any entry point ("" if none). */
+const char* omni_attn_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMNI_ATTN_H */

@@ -1,0 +1,334 @@
+/*
+ * CPU ORACLE — test infrastructure only.
+ *
+ * A plain C restatement of the reference's attention math, used as the checker
+ * for the HIP kernels (tests/, __graft_entry__.smoke(), bench.py's cpu_baseline
+ * leg). Nothing in the product library links, loads or calls this file.
+ *
+ * Functions and the reference code each one restates (paths relative to the
+ * pega-omni tree):
+ *   oracle_slot           crates/omni-qwen3/kernels/qwen3.cu:210-214 (PagedSlots),
+ *                         crates/omni-personaplex/kernels/lm.cu:184-192
+ *   oracle_gather_kv      the same slot rule applied to every key of a row
+ *   oracle_paged_attend   crates/omni-qwen3/kernels/qwen3.cu:123-208 (attend<G>),
+ *                         :234-240 (qwen3_attend), and with `context` the ring cap
+ *                         of crates/omni-personaplex/kernels/lm.cu:273-290
+ *                         (lm_attend, bf16 slots as crates/omni-personaplex/
+ *                         kernels/attend.cuh:41-106)
+ *   oracle_dense_attend   crates/omni-hidream-o1/kernels/hidream.cu:209-347
+ *                         (hidream_attend: base-2 online softmax over 64-key tiles,
+ *                         P rounded to bf16 before P.V, l from unrounded P)
+ *   oracle_fill_normal_bf16 / oracle_splitmix64  the synthetic-input rule
+ *
+ * Arithmetic follows the reference kernels: f32 accumulation, per-tile online
+ * softmax with the same tile sizes (4 warps x 32 keys for the paged kernel, 64
+ * keys for the dense kernel), then bf16 round-to-nearest-even of the output.
+ * Cross-lane sums are taken in butterfly order like the warp reductions.
+ * The exponentials use libm expf / exp2f, so results agree with the GPU
+ * reference to within rounding, not bit for bit.
+ *
+ * Threads: the attention entry points take `nthreads` and split independent
+ * (row, kv head) or (query block, kv head) work items over a pthread pool; the
+ * result does not depend on the thread count.
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef uint16_t bf16_t;
+
+static inline float bf2f(bf16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* Round-to-nearest-even f32 -> bf16 (NaN kept quiet). */
+static inline bf16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+float oracle_bf16_to_f32(bf16_t h) { return bf2f(h); }
+bf16_t oracle_f32_to_bf16(float f) { return f2bf(f); }
+
+/* ---------------------------------------------------------------- inputs */
+
+/* splitmix64 (Steele, Lea, Flood 2014): state += golden gamma, then mix. */
+uint64_t oracle_splitmix64(uint64_t* state) {
+  uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+/* n values of N(0,1) by Box-Muller in double (two uniforms from 53-bit
+ * splitmix64 draws per pair), rounded to bf16 RNE. */
+void oracle_fill_normal_bf16(bf16_t* out, int64_t n, uint64_t seed) {
+  uint64_t st = seed;
+  for (int64_t i = 0; i < n; i += 2) {
+    double u1 = ((oracle_splitmix64(&st) >> 11) + 1.0) * (1.0 / 9007199254740993.0);
+    double u2 = (oracle_splitmix64(&st) >> 11) * (1.0 / 9007199254740992.0);
+    double r = sqrt(-2.0 * log(u1));
+    out[i] = f2bf((float)(r * cos(6.283185307179586 * u2)));
+    if (i + 1 < n) out[i + 1] = f2bf((float)(r * sin(6.283185307179586 * u2)));
+  }
+}
+
+/* ------------------------------------------------------------ page table */
+
+/* Physical slot of logical token t of the row whose page list starts at
+ * pages + indptr[s]: pages[t / page] * page + t % page. */
+int64_t oracle_slot(const int32_t* indptr, const int32_t* pages, int s, int t, int page) {
+  const int32_t* p = pages + indptr[s];
+  return (int64_t)p[t / page] * page + t % page;
+}
+
+/* Dense copy of the first `len` tokens of sequence s: out[t][2*hk][128] =
+ * kv[slot(t)][2*hk][128], byte for byte. */
+void oracle_gather_kv(const bf16_t* kv, int hk, const int32_t* indptr, const int32_t* pages, int page, int s,
+                      int len, bf16_t* out) {
+  const int64_t per = 2LL * hk * 128;
+  for (int t = 0; t < len; ++t) memcpy(out + (int64_t)t * per, kv + oracle_slot(indptr, pages, s, t, page) * per,
+                                       (size_t)per * sizeof(bf16_t));
+}
+
+/* ------------------------------------------------------- thread helper */
+
+typedef void (*item_fn)(void* ctx, int64_t item);
+typedef struct {
+  item_fn fn;
+  void* ctx;
+  int64_t n;
+  int64_t next;
+  pthread_mutex_t mu;
+} pool_t;
+
+static void* pool_worker(void* arg) {
+  pool_t* p = (pool_t*)arg;
+  for (;;) {
+    pthread_mutex_lock(&p->mu);
+    int64_t i = p->next++;
+    pthread_mutex_unlock(&p->mu);
+    if (i >= p->n) return NULL;
+    p->fn(p->ctx, i);
+  }
+}
+
+static void run_items(item_fn fn, void* ctx, int64_t n, int nthreads) {
+  if (nthreads <= 1 || n <= 1) {
+    for (int64_t i = 0; i < n; ++i) fn(ctx, i);
+    return;
+  }
+  pool_t p = {fn, ctx, n, 0, PTHREAD_MUTEX_INITIALIZER};
+  if (nthreads > 256) nthreads = 256;
+  pthread_t th[256];
+  int started = 0;
+  for (int i = 0; i < nthreads; ++i)
+    if (pthread_create(&th[i], NULL, pool_worker, &p) == 0) ++started;
+  if (started == 0) pool_worker(&p);
+  for (int i = 0; i < started; ++i) pthread_join(th[i], NULL);
+}
+
+/* --------------------------------------------------- paged attention */
+
+#define HEAD 128
+#define WARPS 4
+#define LANES 32
+#define GMAX 8
+
+/* Butterfly sum of 32 lane values in the order xor 16, 8, 4, 2, 1 (lane 0's
+ * result), the order a 32-lane xor-shuffle reduction produces. */
+static float bfly_sum(const float* v) {
+  float a[LANES];
+  memcpy(a, v, sizeof a);
+  for (int o = 16; o > 0; o >>= 1) {
+    float b[LANES];
+    for (int l = 0; l < LANES; ++l) b[l] = a[l] + a[l ^ o];
+    memcpy(a, b, sizeof a);
+  }
+  return a[0];
+}
+
+typedef struct {
+  const bf16_t* qkv;
+  const bf16_t* kv;
+  const int32_t* pos;
+  const int32_t* seq;
+  int ragged;
+  const int32_t* indptr;
+  const int32_t* pages;
+  int page;
+  bf16_t* out;
+  int hq, hk;
+  float scale;
+  int context;
+} paged_args;
+
+/* One (row n, kv head kh) work item. Restates attend<G> (qwen3.cu:123-208):
+ * warp w scores the 32-key tiles starting at w*32, w*32+128, ...; each tile
+ * updates (m, l, acc) online with natural exp; the 4 warps' states merge as
+ * num = sum_w acc_w * exp(m_w - top), den = sum_w l_w * exp(m_w - top), with
+ * an empty warp (m = -inf) contributing 0 (attend.cuh:93). */
+static void paged_item(void* vctx, int64_t item) {
+  const paged_args* a = (const paged_args*)vctx;
+  const int n = (int)(item / a->hk), kh = (int)(item % a->hk);
+  const int G = a->hq / a->hk;
+  const int s = a->ragged ? a->seq[n] : n;
+  int len = a->pos[n] + 1;
+  if (len > a->context) len = a->context;
+  const int64_t per_slot = 2LL * a->hk * HEAD;
+  const bf16_t* q = a->qkv + ((int64_t)n * (a->hq + 2 * a->hk) + (int64_t)kh * G) * HEAD;
+  float qs[GMAX][HEAD];
+  for (int g = 0; g < G; ++g)
+    for (int d = 0; d < HEAD; ++d) qs[g][d] = bf2f(q[g * HEAD + d]);
+
+  float M[WARPS][GMAX], L[WARPS][GMAX], O[WARPS][GMAX][HEAD];
+  for (int w = 0; w < WARPS; ++w) {
+    for (int g = 0; g < G; ++g) {
+      float m = -INFINITY, l = 0.f;
+      float* acc = O[w][g];
+      for (int d = 0; d < HEAD; ++d) acc[d] = 0.f;
+      for (int base = w * LANES; base < len; base += WARPS * LANES) {
+        float sv[LANES], p[LANES];
+        int64_t slot[LANES];
+        float tmax = -INFINITY;
+        for (int lane = 0; lane < LANES; ++lane) {
+          const int t = base + lane;
+          const int valid = t < len;
+          slot[lane] = oracle_slot(a->indptr, a->pages, s, valid ? t : base, a->page);
+          const bf16_t* k = a->kv + slot[lane] * per_slot + (int64_t)kh * HEAD;
+          float dot = 0.f;
+          for (int d = 0; d < HEAD; ++d) dot += qs[g][d] * bf2f(k[d]);
+          sv[lane] = valid ? dot * a->scale : -INFINITY;
+          if (sv[lane] > tmax) tmax = sv[lane];
+        }
+        const float m2 = fmaxf(m, tmax);
+        const float corr = expf(m - m2);
+        for (int lane = 0; lane < LANES; ++lane) p[lane] = expf(sv[lane] - m2);
+        l = l * corr + bfly_sum(p);
+        for (int d = 0; d < HEAD; ++d) acc[d] *= corr;
+        m = m2;
+        const int count = len - base < LANES ? len - base : LANES;
+        for (int j = 0; j < count; ++j) {
+          const bf16_t* v = a->kv + slot[j] * per_slot + (int64_t)(a->hk + kh) * HEAD;
+          for (int d = 0; d < HEAD; ++d) acc[d] += p[j] * bf2f(v[d]);
+        }
+      }
+      M[w][g] = m;
+      L[w][g] = l;
+    }
+  }
+  for (int g = 0; g < G; ++g) {
+    float top = -INFINITY;
+    for (int w = 0; w < WARPS; ++w) top = fmaxf(top, M[w][g]);
+    for (int d = 0; d < HEAD; ++d) {
+      float num = 0.f, den = 0.f;
+      for (int w = 0; w < WARPS; ++w) {
+        const float e = M[w][g] == -INFINITY ? 0.f : expf(M[w][g] - top);
+        num += O[w][g][d] * e;
+        den += L[w][g] * e;
+      }
+      a->out[((int64_t)n * a->hq + (int64_t)kh * G + g) * HEAD + d] = f2bf(num / den);
+    }
+  }
+}
+
+/* qwen3_attend / lm_attend (bf16 slots). Row n of sequence s = ragged ? seq[n]
+ * : n sees min(pos[n] + 1, context) keys whose slots come from pages[indptr[s]..].
+ * qkv rows are [(hq + 2 hk)][128] (q heads first); kv slots [2 hk][128];
+ * out [rows][hq][128]. Returns 0, or -1 for an unsupported head shape. */
+int oracle_paged_attend(const bf16_t* qkv, const bf16_t* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                        const int32_t* indptr, const int32_t* pages, int page, bf16_t* out, int rows, int hq, int hk,
+                        float scale, int context, int nthreads) {
+  if (hk <= 0 || hq % hk != 0 || hq / hk > GMAX || page <= 0) return -1;
+  paged_args a = {qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, context > 0 ? context : 0x7fffffff};
+  run_items(paged_item, &a, (int64_t)rows * hk, nthreads);
+  return 0;
+}
+
+/* --------------------------------------------------- dense (DiT) attention */
+
+#define BN 64
+
+typedef struct {
+  const bf16_t* q;
+  const bf16_t* k;
+  const bf16_t* v;
+  bf16_t* out;
+  int q_len, kv_len, q_stride, hq, hk, causal;
+  float scale_log2;
+} dense_args;
+
+/* One (query row n, q head h) item. Restates hidream_attend's per-row math
+ * (hidream.cu:262-344): keys in 64-key tiles up to the block's last key; a
+ * masked score is -inf; per tile m_new = max(m, max_s * scale_log2),
+ * base = m_new or 0 while no key has been seen, alpha = 2^(m - base),
+ * p = 2^(s * scale_log2 - base), l = l * alpha + sum(p) over the unrounded p,
+ * O = O * alpha + bf16(p) . V; finally out = bf16(O * (1 / l)).
+ * The reference's per-thread partial sums of l are merged over the 4 lanes
+ * of a quad at the end; with f32 that changes rounding only. */
+static void dense_item(void* vctx, int64_t item) {
+  const dense_args* a = (const dense_args*)vctx;
+  const int n = (int)(item / a->hq), h = (int)(item % a->hq);
+  const int G = a->hq / a->hk, kvh = h / G;
+  const int kv_stride = a->hk * HEAD;
+  float qs[HEAD], o[HEAD];
+  for (int d = 0; d < HEAD; ++d) {
+    qs[d] = bf2f(a->q[(int64_t)n * a->q_stride + (int64_t)h * HEAD + d]);
+    o[d] = 0.f;
+  }
+  const int lim = a->causal ? (n + 1 < a->kv_len ? n + 1 : a->kv_len) : a->kv_len;
+  float m = -INFINITY, l = 0.f;
+  for (int n0 = 0; n0 < lim; n0 += BN) {
+    float sc[BN];
+    float mx = -INFINITY;
+    for (int j = 0; j < BN; ++j) {
+      const int key = n0 + j;
+      if (key >= lim) {
+        sc[j] = -INFINITY;
+        continue;
+      }
+      const bf16_t* k = a->k + (int64_t)key * kv_stride + (int64_t)kvh * HEAD;
+      float dot = 0.f;
+      for (int d = 0; d < HEAD; ++d) dot += qs[d] * bf2f(k[d]);
+      sc[j] = dot;
+      if (dot > mx) mx = dot;
+    }
+    const float m_new = fmaxf(m, mx * a->scale_log2);
+    const float base = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m - base);
+    m = m_new;
+    float sum = 0.f;
+    for (int j = 0; j < BN; ++j) {
+      sc[j] = exp2f(sc[j] * a->scale_log2 - base);
+      sum += sc[j];
+    }
+    l = l * alpha + sum;
+    for (int d = 0; d < HEAD; ++d) o[d] *= alpha;
+    for (int j = 0; j < BN && n0 + j < lim; ++j) {
+      const float p = bf2f(f2bf(sc[j]));
+      const bf16_t* v = a->v + (int64_t)(n0 + j) * kv_stride + (int64_t)kvh * HEAD;
+      for (int d = 0; d < HEAD; ++d) o[d] += p * bf2f(v[d]);
+    }
+  }
+  const float inv = 1.f / l;
+  for (int d = 0; d < HEAD; ++d) a->out[((int64_t)n * a->hq + h) * HEAD + d] = f2bf(o[d] * inv);
+}
+
+/* hidream_attend generalised to hq = G * hk for any G >= 1 (the reference
+ * fixes G = 4): q rows at q + n * q_stride + h * 128, k and v [kv_len][hk][128],
+ * out [q_len][hq][128]. With causal, row n sees keys 0..min(n, kv_len - 1). */
+int oracle_dense_attend(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_t* out, int q_len, int kv_len,
+                        int q_stride, int hq, int hk, int causal, float scale_log2, int nthreads) {
+  if (hk <= 0 || hq % hk != 0) return -1;
+  dense_args a = {q, k, v, out, q_len, kv_len, q_stride, hq, hk, causal, scale_log2};
+  run_items(dense_item, &a, (int64_t)q_len * hq, nthreads);
+  return 0;
+}

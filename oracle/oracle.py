@@ -1,0 +1,118 @@
+"""CPU oracle bindings — test infrastructure only.
+
+ctypes wrappers around ``liboracle.so`` (built from ``omni_attn_oracle.c`` by
+``oracle/Makefile``), plus numpy helpers for bf16. Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import this
+module; the product library never does.
+
+Every function is a restatement of the reference kernel it names (file:line in
+the pega-omni tree):
+
+* :func:`paged_attend`  — ``crates/omni-qwen3/kernels/qwen3.cu:123-240``
+  (``qwen3_attend``) and, with ``context``, ``crates/omni-personaplex/kernels/
+  lm.cu:273-290`` (``lm_attend``) over bf16 slots (``attend.cuh:41-106``).
+* :func:`dense_attend`  — ``crates/omni-hidream-o1/kernels/hidream.cu:209-347``.
+* :func:`gather_kv` / :func:`slot` — ``qwen3.cu:210-214`` (``PagedSlots``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle.so with gcc (the oracle Makefile)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    return _LIB
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB):
+            build()
+        L = ctypes.CDLL(_LIB)
+        P = ctypes.c_void_p
+        i32, f32, i64, u64 = ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_uint64
+        L.oracle_paged_attend.argtypes = [P, P, P, P, i32, P, P, i32, P, i32, i32, i32, f32, i32, i32]
+        L.oracle_paged_attend.restype = i32
+        L.oracle_dense_attend.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, i32, f32, i32]
+        L.oracle_dense_attend.restype = i32
+        L.oracle_gather_kv.argtypes = [P, i32, P, P, i32, i32, i32, P]
+        L.oracle_gather_kv.restype = None
+        L.oracle_slot.argtypes = [P, P, i32, i32, i32]
+        L.oracle_slot.restype = i64
+        L.oracle_fill_normal_bf16.argtypes = [P, i64, u64]
+        L.oracle_fill_normal_bf16.restype = None
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+# ----------------------------------------------------------------- bf16 helpers
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    """uint16 bf16 bit patterns -> float32 (exact)."""
+    return (a.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(a: np.ndarray) -> np.ndarray:
+    """float32 -> uint16 bf16 bit patterns, round-to-nearest-even."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def normal_bf16(n: int, seed: int) -> np.ndarray:
+    """n draws of N(0,1) (splitmix64 + Box-Muller in double), as bf16 bits."""
+    out = np.empty(n, dtype=np.uint16)
+    lib().oracle_fill_normal_bf16(_p(out), n, seed)
+    return out
+
+
+# ------------------------------------------------------------------ oracle calls
+def paged_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, hq, hk, scale, context=0, nthreads=1):
+    """qwen3_attend / lm_attend over bf16 slots. Arrays are numpy: qkv uint16
+    [rows][(hq+2hk)*128], kv uint16 [slots][2hk*128], int32 index arrays.
+    Returns out uint16 [rows][hq*128]."""
+    rows = int(pos.shape[0])
+    out = np.zeros((rows, hq * 128), dtype=np.uint16)
+    seq = np.ascontiguousarray(seq if seq is not None else np.zeros(rows, np.int32), dtype=np.int32)
+    rc = lib().oracle_paged_attend(_p(qkv), _p(kv), _p(pos), _p(seq), int(ragged), _p(indptr), _p(pages), page,
+                                   _p(out), rows, hq, hk, float(scale), int(context), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_paged_attend: unsupported shape")
+    return out
+
+
+def dense_attend(q, k, v, q_len, kv_len, q_stride, hq, hk, causal, scale_log2, nthreads=1):
+    """hidream_attend: q uint16 rows of q_stride elements, k/v uint16
+    [kv_len][hk*128]. Returns out uint16 [q_len][hq*128]."""
+    out = np.zeros((q_len, hq * 128), dtype=np.uint16)
+    rc = lib().oracle_dense_attend(_p(q), _p(k), _p(v), _p(out), q_len, kv_len, q_stride, hq, hk, int(causal),
+                                   float(scale_log2), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_dense_attend: unsupported shape")
+    return out
+
+
+def gather_kv(kv, hk, indptr, pages, page, s, length):
+    out = np.zeros((length, 2 * hk * 128), dtype=np.uint16)
+    lib().oracle_gather_kv(_p(kv), hk, _p(indptr), _p(pages), page, s, length, _p(out))
+    return out
+
+
+def slot(indptr, pages, s, t, page) -> int:
+    return int(lib().oracle_slot(_p(indptr), _p(pages), s, t, page))

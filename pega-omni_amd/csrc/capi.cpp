@@ -1,0 +1,309 @@
+// The C ABI (include/omni_attn.h): host-side planning and validation, and the
+// entry points the engines bind. Every function returns a status code; the
+// text of the last failure is kept per thread for omni_attn_last_error().
+#include "../../include/omni_attn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[256] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = 0;
+  return OMNI_ATTN_OK;
+}
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+int log2i(int x) {
+  int s = 0;
+  while ((1 << s) < x) ++s;
+  return s;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Split size for a decode bucket. Each (row, kv head) is split into chunks
+// of `chunk` keys so the whole launch has at least ~8k workgroups at full
+// length (32 per CU on 256 CUs), which evens out skewed lengths; chunks
+// stay between 128 and 1024 keys so a workgroup streams >= 64 KiB of K/V.
+int pick_chunk(int rows, int hk, int max_len) {
+  int chunk = 1024;
+  while (chunk > 128) {
+    const long long units = (long long)rows * hk * ((max_len + chunk - 1) / chunk);
+    if (units >= 8192) break;
+    chunk /= 2;
+  }
+  return chunk;
+}
+
+int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                  const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
+                  int context, int len_mode, const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  if (!plan) return fail(OMNI_ATTN_EINVAL, "decode: null plan");
+  if (plan->hq != hq || plan->hk != hk || plan->page != page)
+    return fail(OMNI_ATTN_EINVAL, "decode: plan was made for hq=%d hk=%d page=%d, called with hq=%d hk=%d page=%d",
+                plan->hq, plan->hk, plan->page, hq, hk, page);
+  if (plan->rows == 0) return ok();
+  if (!qkv || !kv || !pos || !indptr || !pages || !out || (ragged && !seq))
+    return fail(OMNI_ATTN_EINVAL, "decode: null device pointer");
+  if (plan->splits > 1 && (!workspace || plan->workspace_bytes <= 0))
+    return fail(OMNI_ATTN_EWORKSPACE, "decode: plan needs %lld workspace bytes", (long long)plan->workspace_bytes);
+  if (!std::isfinite(scale)) return fail(OMNI_ATTN_EINVAL, "decode: non-finite scale");
+  omni::DecodeArgs a{};
+  a.qkv = static_cast<const omni::bf16_t*>(qkv);
+  a.q_stride = (int64_t)(hq + 2 * hk) * OMNI_ATTN_HEAD_DIM;
+  a.kv = static_cast<const omni::bf16_t*>(kv);
+  a.pos = pos;
+  a.seq = seq;
+  a.indptr = indptr;
+  a.pages = pages;
+  a.out = static_cast<omni::bf16_t*>(out);
+  const int64_t o_floats = (int64_t)plan->rows * hq * plan->splits * OMNI_ATTN_HEAD_DIM;
+  a.ws_o = static_cast<float*>(workspace);
+  a.ws_lse = a.ws_o ? a.ws_o + o_floats : nullptr;
+  a.hq = hq;
+  a.hk = hk;
+  a.ragged = ragged ? 1 : 0;
+  a.page_shift = log2i(page);
+  a.context = context > 0 ? context : INT_MAX;
+  a.len_mode = len_mode;
+  a.chunk = plan->chunk;
+  a.splits = plan->splits;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
+  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d not in {1,2,4}", hq / hk);
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(hipGetLastError()));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int omni_attn_version(void) { return 100; }
+
+const char* omni_attn_last_error(void) { return g_err; }
+
+int omni_attn_decode_plan_init(int rows, int hq, int hk, int page, int max_len, int chunk_hint,
+                               omni_attn_decode_plan* plan) {
+  if (!plan) return fail(OMNI_ATTN_EINVAL, "decode_plan: null plan");
+  std::memset(plan, 0, sizeof *plan);
+  if (rows < 0 || rows > 65535) return fail(OMNI_ATTN_EINVAL, "decode_plan: rows=%d outside [0, 65535]", rows);
+  if (hk <= 0 || hq <= 0 || hq % hk != 0)
+    return fail(OMNI_ATTN_EINVAL, "decode_plan: hq=%d is not a multiple of hk=%d", hq, hk);
+  const int G = hq / hk;
+  if (G != 1 && G != 2 && G != 4) return fail(OMNI_ATTN_EUNSUPPORTED, "decode_plan: hq/hk=%d not in {1,2,4}", G);
+  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "decode_plan: page=%d is not a power of two", page);
+  if (max_len <= 0) return fail(OMNI_ATTN_EINVAL, "decode_plan: max_len=%d", max_len);
+  int chunk = chunk_hint > 0 ? chunk_hint : pick_chunk(rows, hk, max_len);
+  if (chunk % 128 != 0) return fail(OMNI_ATTN_EINVAL, "decode_plan: chunk=%d is not a multiple of 128", chunk);
+  plan->rows = rows;
+  plan->hq = hq;
+  plan->hk = hk;
+  plan->page = page;
+  plan->max_len = max_len;
+  plan->chunk = chunk;
+  plan->splits = (max_len + chunk - 1) / chunk;
+  plan->workspace_bytes =
+      plan->splits > 1 ? (int64_t)rows * hq * plan->splits * (OMNI_ATTN_HEAD_DIM + 1) * (int64_t)sizeof(float) : 0;
+  return ok();
+}
+
+int omni_qwen3_attend(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                      const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
+                      const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  return decode_common(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, 0, 0, plan, workspace,
+                       stream);
+}
+
+int omni_lm_attend(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                   const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
+                   int context, const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  if (context <= 0) return fail(OMNI_ATTN_EINVAL, "lm_attend: context=%d", context);
+  return decode_common(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, heads, scale, context, 0, plan,
+                       workspace, stream);
+}
+
+int omni_attn_decode_run_lastlen(const void* qkv, const void* kv, const int32_t* last_page_len, const int32_t* seq,
+                                 int ragged, const int32_t* indptr, const int32_t* pages, int page, void* out, int hq,
+                                 int hk, float scale, const omni_attn_decode_plan* plan, void* workspace,
+                                 void* stream) {
+  return decode_common(qkv, kv, last_page_len, seq, ragged, indptr, pages, page, out, hq, hk, scale, 0, 1, plan,
+                       workspace, stream);
+}
+
+int omni_attn_check_table(const int32_t* indptr_h, int nseqs, const int32_t* pages_h, int num_pages,
+                          const int32_t* pos_h, const int32_t* seq_h, int ragged, int rows, int page, int context) {
+  if (!indptr_h || nseqs < 0 || num_pages < 0 || rows < 0 || page <= 0)
+    return fail(OMNI_ATTN_EINVAL, "check_table: bad arguments");
+  if (indptr_h[0] != 0) return fail(OMNI_ATTN_ETABLE, "check_table: indptr[0]=%d, expected 0", indptr_h[0]);
+  for (int s = 0; s < nseqs; ++s)
+    if (indptr_h[s + 1] < indptr_h[s])
+      return fail(OMNI_ATTN_ETABLE, "check_table: indptr not monotone at %d (%d > %d)", s, indptr_h[s],
+                  indptr_h[s + 1]);
+  if (pages_h) {
+    for (int i = 0; i < indptr_h[nseqs]; ++i)
+      if (pages_h[i] < 0 || pages_h[i] >= num_pages)
+        return fail(OMNI_ATTN_ETABLE, "check_table: page id %d at %d outside [0, %d)", pages_h[i], i, num_pages);
+  }
+  if (pos_h) {
+    for (int n = 0; n < rows; ++n) {
+      const int s = ragged ? (seq_h ? seq_h[n] : -1) : n;
+      if (s < 0 || s >= nseqs) return fail(OMNI_ATTN_ETABLE, "check_table: row %d names sequence %d", n, s);
+      if (pos_h[n] < 0) return fail(OMNI_ATTN_ETABLE, "check_table: row %d at negative position %d", n, pos_h[n]);
+      long long len = (long long)pos_h[n] + 1;
+      if (context > 0 && len > context) len = context;
+      const long long have = (long long)(indptr_h[s + 1] - indptr_h[s]) * page;
+      if (len > have)
+        return fail(OMNI_ATTN_ETABLE, "check_table: row %d needs %lld tokens, sequence %d has pages for %lld", n, len,
+                    s, have);
+    }
+  }
+  return ok();
+}
+
+int omni_attn_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int page,
+                        const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
+                        void* stream) {
+  if (nseq < 0 || hk <= 0) return fail(OMNI_ATTN_EINVAL, "gather_kv: nseq=%d hk=%d", nseq, hk);
+  if (nseq == 0) return ok();
+  if (!kv || !indptr || !pages || !seq_ids || !lens || !out_indptr || !out)
+    return fail(OMNI_ATTN_EINVAL, "gather_kv: null device pointer");
+  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "gather_kv: page=%d is not a power of two", page);
+  if (omni::launch_gather_kv(kv, hk, indptr, pages, log2i(page), seq_ids, lens, out_indptr, nseq, out,
+                             as_stream(stream)) != 0)
+    return fail(OMNI_ATTN_ELAUNCH, "gather_kv: launch failed");
+  return ok();
+}
+
+
+int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_t* seq_h, const int32_t* pos_h,
+                                int32_t* work_h, int64_t work_cap, omni_attn_prefill_plan* plan) {
+  if (!plan) return fail(OMNI_ATTN_EINVAL, "prefill_plan: null plan");
+  std::memset(plan, 0, sizeof *plan);
+  if (rows < 0) return fail(OMNI_ATTN_EINVAL, "prefill_plan: rows=%d", rows);
+  if (hk <= 0 || hq <= 0 || hq % hk != 0)
+    return fail(OMNI_ATTN_EINVAL, "prefill_plan: hq=%d is not a multiple of hk=%d", hq, hk);
+  const int G = hq / hk;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: hq/hk=%d not in {1,2,4,8}", G);
+  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: page=%d is not a power of two", page);
+  if (rows > 0 && (!seq_h || !pos_h)) return fail(OMNI_ATTN_EINVAL, "prefill_plan: null host arrays");
+  const int per_tile = omni::kTiledRows / G;  // query positions per tile
+  plan->rows = rows;
+  plan->hq = hq;
+  plan->hk = hk;
+  plan->page = page;
+  plan->tile_rows = omni::kTiledRows;
+  // Runs of rows of one sequence at consecutive positions, cut into tiles.
+  int64_t tiles = 0;
+  for (int n = 0; n < rows;) {
+    int e = n + 1;
+    if (pos_h[n] < 0) return fail(OMNI_ATTN_ETABLE, "prefill_plan: row %d at negative position %d", n, pos_h[n]);
+    while (e < rows && seq_h[e] == seq_h[n] && pos_h[e] == pos_h[e - 1] + 1) ++e;
+    for (int f = n; f < e; f += per_tile) {
+      if (work_h && (tiles + 1) * 4 <= work_cap) {
+        work_h[tiles * 4 + 0] = seq_h[n];
+        work_h[tiles * 4 + 1] = f;
+        work_h[tiles * 4 + 2] = (e - f) < per_tile ? (e - f) : per_tile;
+        work_h[tiles * 4 + 3] = 0;
+      }
+      ++tiles;
+    }
+    n = e;
+  }
+  if (tiles > INT_MAX / 4) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: too many tiles");
+  plan->tiles = (int32_t)tiles;
+  plan->work_bytes = tiles * 4 * (int64_t)sizeof(int32_t);
+  if (!work_h || tiles * 4 > work_cap)
+    return fail(OMNI_ATTN_EWORKSPACE, "prefill_plan: work list needs %lld int32", (long long)(tiles * 4));
+  return ok();
+}
+
+int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, const void* kv, const int32_t* pos,
+                          const int32_t* seq, const int32_t* indptr, const int32_t* pages, void* out, float scale,
+                          const int32_t* work, void* stream) {
+  if (!plan) return fail(OMNI_ATTN_EINVAL, "prefill_run: null plan");
+  if (plan->tiles == 0) return ok();
+  if (!qkv || !kv || !pos || !seq || !indptr || !pages || !out || !work)
+    return fail(OMNI_ATTN_EINVAL, "prefill_run: null device pointer");
+  omni::TiledArgs a{};
+  a.q = static_cast<const omni::bf16_t*>(qkv);
+  a.q_stride = (int64_t)(plan->hq + 2 * plan->hk) * OMNI_ATTN_HEAD_DIM;
+  a.kv = static_cast<const omni::bf16_t*>(kv);
+  a.pos = pos;
+  a.seq = seq;
+  a.indptr = indptr;
+  a.pages = pages;
+  a.work = work;
+  a.page_shift = log2i(plan->page);
+  a.causal = 1;
+  a.out = static_cast<omni::bf16_t*>(out);
+  a.hq = plan->hq;
+  a.hk = plan->hk;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int rc = omni::launch_prefill(a, plan->tiles, as_stream(stream));
+  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_run: shape not implemented");
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "prefill_run: launch failed");
+  return ok();
+}
+
+int omni_hidream_attend_batched(const void* q, const void* k, const void* v, void* out, int q_len,
+                                const int32_t* kv_len_at, int q_stride, int causal, float scale_log2, int hq, int hk,
+                                int batch, int64_t q_bstride, int64_t kv_bstride, int64_t out_bstride, void* stream) {
+  if (q_len < 0 || batch < 0) return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_len=%d batch=%d", q_len, batch);
+  if (q_len == 0 || batch == 0) return ok();
+  if (!q || !k || !v || !out || !kv_len_at) return fail(OMNI_ATTN_EINVAL, "hidream_attend: null device pointer");
+  if (hk <= 0 || hq <= 0 || hq % hk != 0)
+    return fail(OMNI_ATTN_EINVAL, "hidream_attend: hq=%d is not a multiple of hk=%d", hq, hk);
+  const int G = hq / hk;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: hq/hk=%d not in {1,2,4,8}", G);
+  if (q_stride < hq * OMNI_ATTN_HEAD_DIM || q_stride % 8 != 0)
+    return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_stride=%d", q_stride);
+  if (batch > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: batch=%d", batch);
+  omni::TiledArgs a{};
+  a.q = static_cast<const omni::bf16_t*>(q);
+  a.q_stride = q_stride;
+  a.k = static_cast<const omni::bf16_t*>(k);
+  a.v = static_cast<const omni::bf16_t*>(v);
+  a.kv_len_at = kv_len_at;
+  a.q_len = q_len;
+  a.causal = causal ? 1 : 0;
+  a.q_bstride = q_bstride;
+  a.kv_bstride = kv_bstride;
+  a.out_bstride = out_bstride;
+  a.out = static_cast<omni::bf16_t*>(out);
+  a.hq = hq;
+  a.hk = hk;
+  a.scale_log2 = scale_log2;
+  const int rc = omni::launch_dit(a, batch, as_stream(stream));
+  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: shape not implemented");
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed");
+  return ok();
+}
+
+int omni_hidream_attend(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
+                        int q_stride, int causal, float scale_log2, int hq, int hk, void* stream) {
+  return omni_hidream_attend_batched(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, 1, 0, 0, 0,
+                                     stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,254 @@
+// Paged GQA / MHA decode attention for gfx950: split-K over keys, bandwidth
+// bound, no MFMA (one query token per row is a GEMV per K/V head).
+//
+// Semantics are those of qwen3_attend (crates/omni-qwen3/kernels/qwen3.cu:
+// 123-240) and lm_attend over bf16 slots (crates/omni-personaplex/kernels/
+// lm.cu:273-290): row n of sequence s = ragged ? seq[n] : n sees the first
+// min(pos[n] + 1, context) tokens of s, token t in slot
+// pages[indptr[s] + t / page] * page + t % page, slot = [K heads | V heads][128].
+//
+// Work: one workgroup of four waves per (split, kv head, row). A split is
+// `chunk` consecutive keys; wave w takes 32-key tiles w, w + 4, ... of it.
+// Within a wave, lane (r, c) = (lane / 16, lane % 16) owns the 16-byte chunk c
+// (8 of 128 dims) of keys 4 i + r of the tile, i = 0..7: each row of 16 lanes
+// reads one key's 256-byte K (and V) head row with one coalesced 16-byte load
+// per lane, so every load instruction moves four whole 256-byte rows.
+// Scores: per-lane partial dot products of the G query heads sharing the K/V
+// head, summed over the 16 lanes of a DPP row. Softmax: base 2 with the scale
+// folded into q, online per tile, the running max shared by the whole wave.
+// V: each lane accumulates p * v for its 8 dims and G heads; rows merge at the
+// end, waves merge in LDS, splits merge in `decode_combine` (log-sum-exp).
+#include "common.h"
+#include "kernels.h"
+
+namespace omni {
+
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeThreads = kDecodeWaves * 64;
+constexpr int kTileKeys = 32;
+
+__device__ __forceinline__ int decode_len(const DecodeArgs& a, int n, int s) {
+  int len;
+  if (a.len_mode == 0)
+    len = a.pos[n] + 1;
+  else
+    len = ((a.indptr[s + 1] - a.indptr[s] - 1) << a.page_shift) + a.pos[s];
+  return min(len, a.context);
+}
+
+__device__ __forceinline__ int decode_nsplit(const DecodeArgs& a, int len) {
+  return len <= a.chunk ? 1 : min(a.splits, (len + a.chunk - 1) / a.chunk);
+}
+
+template <int G>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
+  const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
+  const int s = a.ragged ? a.seq[n] : n;
+  const int len = decode_len(a, n, s);
+  const int nsplit = decode_nsplit(a, len);
+  if (split >= nsplit) return;
+  const int t0 = split * a.chunk;
+  const int t1 = split == nsplit - 1 ? len : t0 + a.chunk;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane >> 4, c = lane & 15;
+
+  float q[G][8];
+  const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * G * kHead + c * 8;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    widen8(ldg16(qp + g * kHead), q[g]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[g][e] *= a.scale_log2;
+  }
+
+  const int32_t* pg = a.pages + a.indptr[s];
+  const int64_t per_slot = 2LL * a.hk * kHead;
+  const bf16_t* kb = a.kv + (int64_t)kh * kHead + c * 8;
+  const bf16_t* vb = a.kv + (int64_t)(a.hk + kh) * kHead + c * 8;
+  const int shift = a.page_shift, pmask = (1 << shift) - 1;
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+
+  for (int tb = t0 + wave * kTileKeys; tb < t1; tb += kDecodeWaves * kTileKeys) {
+    int64_t off[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int t = tb + 4 * i + r;
+      t = t < t1 ? t : tb;  // keys past the split read a valid row; their p is 0
+      off[i] = ((((int64_t)pg[t >> shift]) << shift) | (t & pmask)) * per_slot;
+    }
+    uint4 kr[8], vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = ldg16(kb + off[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vr[i] = ldg16(vb + off[i]);
+
+    float sc[G][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float kf[8];
+      widen8(kr[i], kf);
+      const bool valid = tb + 4 * i + r < t1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(q[g][e], kf[e], d);
+        d = row16_sum(d);
+        sc[g][i] = valid ? d : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = sc[g][0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[g][i]);
+      mx = fmaxf(mx, xor_lane(mx, 16));
+      mx = fmaxf(mx, xor_lane(mx, 32));
+      const float mn = fmaxf(m[g], mx);
+      const float corr = fast_exp2(m[g] - mn);
+      m[g] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        sc[g][i] = fast_exp2(sc[g][i] - mn);
+        ps += sc[g][i];
+      }
+      l[g] = fmaf(l[g], corr, ps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= corr;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float vf[8];
+      widen8(vr[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(sc[g][i], vf[e], acc[g][e]);
+    }
+  }
+
+  // Rows of the wave hold disjoint keys under one shared max: add them up.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] += xor_lane(l[g], 16);
+    l[g] += xor_lane(l[g], 32);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      acc[g][e] += xor_lane(acc[g][e], 16);
+      acc[g][e] += xor_lane(acc[g][e], 32);
+    }
+  }
+
+  __shared__ float sm_m[kDecodeWaves][G], sm_l[kDecodeWaves][G];
+  __shared__ float sm_o[kDecodeWaves][G][kHead];
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm_o[wave][g][c * 8 + e] = acc[g][e];
+      if (c == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * kHead; i += kDecodeThreads) {
+    const int g = i / kHead, d = i % kHead;
+    float top = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) top = fmaxf(top, sm_m[w][g]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float e = sm_m[w][g] == -INFINITY ? 0.f : fast_exp2(sm_m[w][g] - top);
+      num = fmaf(sm_o[w][g][d], e, num);
+      den = fmaf(sm_l[w][g], e, den);
+    }
+    const int64_t h = (int64_t)n * a.hq + kh * G + g;
+    if (nsplit == 1) {
+      a.out[h * kHead + d] = (bf16_t)f2bf(len > 0 ? num / den : 0.f);
+    } else {
+      a.ws_o[(h * a.splits + split) * kHead + d] = num / den;
+      if (d == 0) a.ws_lse[h * a.splits + split] = top + __log2f(den);
+    }
+  }
+}
+
+// Merge the splits of every (row, q head) that used more than one.
+__global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
+  const int h = blockIdx.x, n = blockIdx.y, d = threadIdx.x;
+  const int s = a.ragged ? a.seq[n] : n;
+  const int len = decode_len(a, n, s);
+  const int nsplit = decode_nsplit(a, len);
+  if (nsplit <= 1) return;
+  const int64_t hh = (int64_t)n * a.hq + h;
+  const float* lse = a.ws_lse + hh * a.splits;
+  float top = -INFINITY;
+  for (int i = 0; i < nsplit; ++i) top = fmaxf(top, lse[i]);
+  float num = 0.f, den = 0.f;
+  for (int i = 0; i < nsplit; ++i) {
+    const float w = fast_exp2(lse[i] - top);
+    den += w;
+    num = fmaf(w, a.ws_o[(hh * a.splits + i) * kHead + d], num);
+  }
+  a.out[hh * kHead + d] = (bf16_t)f2bf(num / den);
+}
+
+int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
+  const dim3 grid(a.splits, a.hk, rows);
+  switch (a.hq / a.hk) {
+    case 1: decode_split<1><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+    case 2: decode_split<2><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+    case 4: decode_split<4><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+    default: return -2;
+  }
+  if (hipGetLastError() != hipSuccess) return -3;
+  if (a.splits > 1) {
+    decode_combine<<<dim3(a.hq, rows), kHead, 0, stream>>>(a);
+    if (hipGetLastError() != hipSuccess) return -3;
+  }
+  return 0;
+}
+
+// ------------------------------------------------------------------ gather
+
+// Block per sequence i: copy its first lens[i] tokens' slots to dense rows.
+// Each slot is 2 * hk * 256 bytes, copied as 16-byte words.
+__global__ __launch_bounds__(256) void gather_kv_kernel(const uint4* kv, int hk, const int32_t* indptr,
+                                                        const int32_t* pages, int shift, const int32_t* seq_ids,
+                                                        const int32_t* lens, const int32_t* out_indptr, uint4* out) {
+  const int i = blockIdx.x;
+  const int s = seq_ids[i], len = lens[i];
+  const int64_t words = 2LL * hk * kHead * 2 / 16;
+  const int32_t* pg = pages + indptr[s];
+  const int pmask = (1 << shift) - 1;
+  uint4* dst = out + (int64_t)out_indptr[i] * words;
+  const int64_t total = (int64_t)len * words;
+  for (int64_t w = blockIdx.y * 256 + threadIdx.x; w < total; w += (int64_t)gridDim.y * 256) {
+    const int t = (int)(w / words);
+    const int64_t slot = ((int64_t)pg[t >> shift] << shift) | (t & pmask);
+    dst[w] = kv[slot * words + (w % words)];
+  }
+}
+
+int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int shift,
+                     const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
+                     hipStream_t stream) {
+  if (nseq == 0) return 0;
+  gather_kv_kernel<<<dim3(nseq, 16), 256, 0, stream>>>(static_cast<const uint4*>(kv), hk, indptr, pages, shift,
+                                                      seq_ids, lens, out_indptr, static_cast<uint4*>(out));
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+}  // namespace omni

@@ -1,0 +1,66 @@
+// Launch interface between the C ABI (capi.cpp) and the HIP kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace omni {
+
+typedef uint16_t bf16_t;
+
+// Everything a decode launch reads; passed by value as the kernel argument.
+struct DecodeArgs {
+  const bf16_t* qkv;
+  int64_t q_stride;  // elements between consecutive qkv rows
+  const bf16_t* kv;
+  const int32_t* pos;  // len_mode 0: per-row positions; 1: per-sequence last page lengths
+  const int32_t* seq;
+  const int32_t* indptr;
+  const int32_t* pages;
+  bf16_t* out;
+  float* ws_o;   // [rows][hq][splits][128] split outputs (normalised)
+  float* ws_lse; // [rows][hq][splits] split log2-sum-exp
+  int hq, hk;
+  int ragged;
+  int page_shift;
+  int context;  // cap on keys per row
+  int len_mode;
+  int chunk, splits;
+  float scale_log2;  // softmax scale times log2(e)
+};
+
+int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream);
+
+int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int shift,
+                     const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
+                     hipStream_t stream);
+
+// Tiled MFMA attention (prefill and DiT).
+struct TiledArgs {
+  const bf16_t* q;
+  int64_t q_stride;  // elements between query rows
+  // paged source (mode 0): kv slots [2 hk][128]
+  const bf16_t* kv;
+  const int32_t* pos;
+  const int32_t* seq;
+  const int32_t* indptr;
+  const int32_t* pages;
+  const int32_t* work;  // 4 int32 per tile: seq, first row, rows, unused
+  int page_shift;
+  // dense source (mode 1): k, v [slots][hk][128]
+  const bf16_t* k;
+  const bf16_t* v;
+  const int32_t* kv_len_at;
+  int q_len;
+  int causal;
+  int64_t q_bstride, kv_bstride, out_bstride;
+  bf16_t* out;
+  int hq, hk;
+  float scale_log2;
+};
+
+constexpr int kTiledRows = 128;  // packed (position, head) query rows per MFMA tile
+
+int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream);
+int launch_dit(const TiledArgs& a, int batch, hipStream_t stream);
+
+}  // namespace omni

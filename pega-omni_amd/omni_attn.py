@@ -1,0 +1,270 @@
+"""Host-side mirror of the engines' attention ops over the C ABI.
+
+The reference engines launch ``qwen3_attend`` (crates/omni-qwen3/src/stack.rs:
+207-241), ``lm_attend`` (crates/omni-personaplex/src/helium.rs:256-275) and
+``hidream_attend`` (crates/omni-hidream-o1/src/model.rs:362-380) with raw
+device pointers. This module exposes the same calls, argument for argument,
+over ``libomni_attn.so`` via ctypes, taking torch tensors only as holders of
+device memory and streams. There is no fallback: if the HIP library is absent
+or a launch fails, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libomni_attn.so")
+HEAD_DIM = 128
+
+OK = 0
+EINVAL = -1
+EUNSUPPORTED = -2
+ELAUNCH = -3
+EWORKSPACE = -4
+ETABLE = -5
+
+EXPORTS = (
+    "omni_attn_decode_plan_init",
+    "omni_qwen3_attend",
+    "omni_lm_attend",
+    "omni_attn_decode_run_lastlen",
+    "omni_attn_check_table",
+    "omni_attn_gather_kv",
+    "omni_attn_prefill_plan_init",
+    "omni_attn_prefill_run",
+    "omni_hidream_attend",
+    "omni_hidream_attend_batched",
+    "omni_attn_version",
+    "omni_attn_last_error",
+)
+
+
+class OmniAttnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"omni_attn error {code}: {msg}")
+        self.code = code
+
+
+class DecodePlan(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int32),
+        ("hq", ctypes.c_int32),
+        ("hk", ctypes.c_int32),
+        ("page", ctypes.c_int32),
+        ("max_len", ctypes.c_int32),
+        ("chunk", ctypes.c_int32),
+        ("splits", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_int64),
+    ]
+
+
+class PrefillPlan(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int32),
+        ("hq", ctypes.c_int32),
+        ("hk", ctypes.c_int32),
+        ("page", ctypes.c_int32),
+        ("tiles", ctypes.c_int32),
+        ("tile_rows", ctypes.c_int32),
+        ("work_bytes", ctypes.c_int64),
+    ]
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load the HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise OmniAttnError(ELAUNCH, f"{path} is missing: build it with pega-omni_amd/build.py")
+    L = ctypes.CDLL(path)
+    P, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    dplan = ctypes.POINTER(DecodePlan)
+    pplan = ctypes.POINTER(PrefillPlan)
+    sig = {
+        "omni_attn_decode_plan_init": [i32, i32, i32, i32, i32, i32, dplan],
+        "omni_qwen3_attend": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
+        "omni_lm_attend": [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, dplan, P, P],
+        "omni_attn_decode_run_lastlen": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
+        "omni_attn_check_table": [P, i32, P, i32, P, P, i32, i32, i32, i32],
+        "omni_attn_gather_kv": [P, i32, P, P, i32, P, P, P, i32, P, P],
+        "omni_attn_prefill_plan_init": [i32, i32, i32, i32, P, P, P, i64, pplan],
+        "omni_attn_prefill_run": [pplan, P, P, P, P, P, P, P, f32, P, P],
+        "omni_hidream_attend": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, P],
+        "omni_hidream_attend_batched": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, i32, i64, i64, i64, P],
+        "omni_attn_version": [],
+        "omni_attn_last_error": [],
+    }
+    for name, args in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_char_p if name == "omni_attn_last_error" else ctypes.c_int
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != OK:
+        raise OmniAttnError(rc, load().omni_attn_last_error().decode())
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _bf16_dev(t, name):
+    import torch
+
+    if t.dtype != torch.bfloat16 or not t.is_cuda or not t.is_contiguous():
+        raise OmniAttnError(EINVAL, f"{name} must be a contiguous bf16 device tensor")
+
+
+def _i32_dev(t, name):
+    import torch
+
+    if t is None:
+        return
+    if t.dtype != torch.int32 or not t.is_cuda or not t.is_contiguous():
+        raise OmniAttnError(EINVAL, f"{name} must be a contiguous int32 device tensor")
+
+
+# --------------------------------------------------------------------- decode
+def decode_plan(rows: int, hq: int, hk: int, page: int, max_len: int, chunk: int = 0) -> DecodePlan:
+    plan = DecodePlan()
+    _check(load().omni_attn_decode_plan_init(rows, hq, hk, page, max_len, chunk, ctypes.byref(plan)))
+    return plan
+
+
+def workspace_for(plan, device="cuda"):
+    """Device workspace for a plan (None when the plan needs none)."""
+    import torch
+
+    n = int(plan.workspace_bytes)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def check_table(indptr_h, pages_h, num_pages, pos_h=None, seq_h=None, ragged=False, page=16, context=0):
+    """Host validation of a page table (numpy int32 arrays)."""
+    import numpy as np
+
+    indptr_h = np.ascontiguousarray(indptr_h, dtype=np.int32)
+    pages_h = np.ascontiguousarray(pages_h, dtype=np.int32)
+    rows = 0 if pos_h is None else len(pos_h)
+    pos_a = None if pos_h is None else np.ascontiguousarray(pos_h, dtype=np.int32)
+    seq_a = None if seq_h is None else np.ascontiguousarray(seq_h, dtype=np.int32)
+    rc = load().omni_attn_check_table(
+        indptr_h.ctypes.data_as(ctypes.c_void_p), len(indptr_h) - 1, pages_h.ctypes.data_as(ctypes.c_void_p),
+        num_pages, None if pos_a is None else pos_a.ctypes.data_as(ctypes.c_void_p),
+        None if seq_a is None else seq_a.ctypes.data_as(ctypes.c_void_p), int(ragged), rows, page, context)
+    _check(rc)
+
+
+def qwen3_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, plan, workspace=None,
+                 stream=None):
+    """``qwen3_attend`` (crates/omni-qwen3/kernels/qwen3.cu:234-240) on the GPU."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
+    for t, n in ((pos, "pos"), (seq, "seq"), (indptr, "indptr"), (pages, "pages")):
+        _i32_dev(t, n)
+    _check(load().omni_qwen3_attend(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr),
+                                    _ptr(pages), page, _ptr(out), hq, hk, float(scale), ctypes.byref(plan),
+                                    _ptr(workspace), _stream(stream)))
+    return out
+
+
+def lm_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, scale, context, plan, workspace=None,
+              stream=None):
+    """``lm_attend`` (crates/omni-personaplex/kernels/lm.cu:275-290) over bf16 slots."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
+    for t, n in ((pos, "pos"), (seq, "seq"), (indptr, "indptr"), (pages, "pages")):
+        _i32_dev(t, n)
+    _check(load().omni_lm_attend(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr), _ptr(pages),
+                                 page, _ptr(out), heads, float(scale), context, ctypes.byref(plan), _ptr(workspace),
+                                 _stream(stream)))
+    return out
+
+
+def decode_lastlen(qkv, kv, last_page_len, seq, ragged, indptr, pages, page, out, hq, hk, scale, plan,
+                   workspace=None, stream=None):
+    """Decode with per-sequence last-page lengths instead of positions."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
+    _check(load().omni_attn_decode_run_lastlen(_ptr(qkv), _ptr(kv), _ptr(last_page_len), _ptr(seq), int(ragged),
+                                               _ptr(indptr), _ptr(pages), page, _ptr(out), hq, hk, float(scale),
+                                               ctypes.byref(plan), _ptr(workspace), _stream(stream)))
+    return out
+
+
+def gather_kv(kv, hk, indptr, pages, page, seq_ids, lens, out_indptr, out, stream=None):
+    """Bit-exact paged -> dense copy of K/V slots (the page-table rule)."""
+    nseq = int(seq_ids.numel())
+    _check(load().omni_attn_gather_kv(_ptr(kv), hk, _ptr(indptr), _ptr(pages), page, _ptr(seq_ids), _ptr(lens),
+                                      _ptr(out_indptr), nseq, _ptr(out), _stream(stream)))
+    return out
+
+
+# -------------------------------------------------------------------- prefill
+@dataclass
+class Prefill:
+    plan: PrefillPlan
+    work: object  # device int32 tensor
+
+
+def prefill_plan(rows, hq, hk, page, seq_h, pos_h, device="cuda") -> Prefill:
+    """Host plan of a ragged causal prefill; uploads the work list."""
+    import numpy as np
+    import torch
+
+    seq_a = np.ascontiguousarray(seq_h, dtype=np.int32)
+    pos_a = np.ascontiguousarray(pos_h, dtype=np.int32)
+    plan = PrefillPlan()
+    L = load()
+    rc = L.omni_attn_prefill_plan_init(rows, hq, hk, page, seq_a.ctypes.data_as(ctypes.c_void_p),
+                                       pos_a.ctypes.data_as(ctypes.c_void_p), None, 0, ctypes.byref(plan))
+    if rc not in (OK, EWORKSPACE):
+        _check(rc)
+    cap = max(1, int(plan.work_bytes) // 4)
+    work_h = np.zeros(cap, dtype=np.int32)
+    _check(L.omni_attn_prefill_plan_init(rows, hq, hk, page, seq_a.ctypes.data_as(ctypes.c_void_p),
+                                         pos_a.ctypes.data_as(ctypes.c_void_p),
+                                         work_h.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(plan)))
+    return Prefill(plan, torch.from_numpy(work_h).to(device))
+
+
+def prefill_run(pf: Prefill, qkv, kv, pos, seq, indptr, pages, out, scale, stream=None):
+    """Ragged causal prefill with qwen3_attend(ragged = 1) semantics (MFMA)."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
+    _check(load().omni_attn_prefill_run(ctypes.byref(pf.plan), _ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq),
+                                        _ptr(indptr), _ptr(pages), _ptr(out), float(scale), _ptr(pf.work),
+                                        _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------------------------ DiT
+def hidream_attend(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, stream=None):
+    """``hidream_attend`` (crates/omni-hidream-o1/kernels/hidream.cu:209-347)."""
+    _check(load().omni_hidream_attend(_ptr(q), _ptr(k), _ptr(v), _ptr(out), q_len, _ptr(kv_len_at), q_stride,
+                                      int(causal), float(scale_log2), hq, hk, _stream(stream)))
+    return out
+
+
+def hidream_attend_batched(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, batch, q_bstride,
+                           kv_bstride, out_bstride, stream=None):
+    _check(load().omni_hidream_attend_batched(_ptr(q), _ptr(k), _ptr(v), _ptr(out), q_len, _ptr(kv_len_at), q_stride,
+                                              int(causal), float(scale_log2), hq, hk, batch, q_bstride, kv_bstride,
+                                              out_bstride, _stream(stream)))
+    return out

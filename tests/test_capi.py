@@ -1,0 +1,131 @@
+"""The C ABI without a GPU: the library loads, exports every entry point the
+header declares, and its host-side planning and validation behave as
+documented (no kernel launches here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import omni_attn as oa
+import workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "omni_attn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(omni_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_what_python_binds():
+    assert set(declared_functions()) == set(oa.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = oa.load()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    assert L.omni_attn_version() >= 100
+
+
+def test_decode_plan_shapes():
+    p = oa.decode_plan(128, 32, 32, 16, 3000)
+    assert p.splits == (3000 + p.chunk - 1) // p.chunk and p.chunk % 128 == 0
+    assert p.workspace_bytes == 128 * 32 * p.splits * 129 * 4
+    p1 = oa.decode_plan(4, 16, 8, 16, 100)
+    assert p1.splits == 1 and p1.workspace_bytes == 0
+    p2 = oa.decode_plan(4, 16, 8, 16, 1000, chunk=256)
+    assert p2.chunk == 256 and p2.splits == 4
+
+
+@pytest.mark.parametrize("args,code", [
+    ((4, 16, 6, 16, 100, 0), oa.EINVAL),        # hq not a multiple of hk
+    ((4, 16, 2, 16, 100, 0), oa.EUNSUPPORTED),  # G = 8 not implemented in decode
+    ((4, 16, 8, 12, 100, 0), oa.EUNSUPPORTED),  # page not a power of two
+    ((4, 16, 8, 16, 0, 0), oa.EINVAL),          # max_len
+    ((4, 16, 8, 16, 100, 100), oa.EINVAL),      # chunk not a multiple of 128
+    ((70000, 16, 8, 16, 100, 0), oa.EINVAL),    # rows beyond grid limit
+])
+def test_decode_plan_rejects(args, code):
+    with pytest.raises(oa.OmniAttnError) as e:
+        oa.decode_plan(*args)
+    assert e.value.code == code
+
+
+def test_run_without_workspace_fails_before_launch():
+    p = oa.decode_plan(4, 16, 8, 16, 1000, chunk=128)
+    fake = ctypes.c_void_p(16)
+    rc = oa.load().omni_qwen3_attend(fake, fake, fake, None, 0, fake, fake, 16, fake, 16, 8, 0.1, ctypes.byref(p),
+                                     None, None)
+    assert rc == oa.EWORKSPACE
+    rc = oa.load().omni_qwen3_attend(fake, fake, fake, None, 0, fake, fake, 16, fake, 16, 4, 0.1, ctypes.byref(p),
+                                     None, None)
+    assert rc == oa.EINVAL  # plan/argument mismatch
+    rc = oa.load().omni_qwen3_attend(None, fake, fake, None, 0, fake, fake, 16, fake, 16, 8, 0.1, ctypes.byref(p),
+                                     fake, None)
+    assert rc == oa.EINVAL
+
+
+def test_check_table_accepts_generated_cases():
+    c = W.paged_decode_case(9, 8, 4, 1, 500, seed=1)
+    oa.check_table(c.indptr, c.pages, c.num_pages, c.pos, None, False, 16)
+    r = W.ragged_prefill_case(3, 8, 2, 5, 60, 0, 40, seed=2)
+    oa.check_table(r.indptr, r.pages, r.num_pages, r.pos, r.seq, True, 16)
+
+
+def test_check_table_rejects_bad_tables():
+    c = W.paged_decode_case(4, 8, 4, 20, 100, seed=3)
+    bad = c.indptr.copy()
+    bad[2] = bad[3] + 1
+    with pytest.raises(oa.OmniAttnError) as e:
+        oa.check_table(bad, c.pages, c.num_pages, c.pos, None, False, 16)
+    assert e.value.code == oa.ETABLE
+    pages = c.pages.copy()
+    pages[1] = c.num_pages
+    with pytest.raises(oa.OmniAttnError):
+        oa.check_table(c.indptr, pages, c.num_pages, c.pos, None, False, 16)
+    pos = c.pos.copy()
+    pos[0] = (c.indptr[1] - c.indptr[0]) * 16  # one token past its pages
+    with pytest.raises(oa.OmniAttnError):
+        oa.check_table(c.indptr, c.pages, c.num_pages, pos, None, False, 16)
+    # ...unless the ring cap keeps it inside.
+    oa.check_table(c.indptr, c.pages, c.num_pages, pos, None, False, 16, context=int(c.pos[0]) + 1)
+
+
+def _plan_host(rows, hq, hk, seq, pos):
+    L = oa.load()
+    plan = oa.PrefillPlan()
+    seq = np.ascontiguousarray(seq, np.int32)
+    pos = np.ascontiguousarray(pos, np.int32)
+    rc = L.omni_attn_prefill_plan_init(rows, hq, hk, 16, seq.ctypes.data_as(ctypes.c_void_p),
+                                       pos.ctypes.data_as(ctypes.c_void_p), None, 0, ctypes.byref(plan))
+    assert rc == oa.EWORKSPACE
+    work = np.zeros(plan.work_bytes // 4, np.int32)
+    rc = L.omni_attn_prefill_plan_init(rows, hq, hk, 16, seq.ctypes.data_as(ctypes.c_void_p),
+                                       pos.ctypes.data_as(ctypes.c_void_p), work.ctypes.data_as(ctypes.c_void_p),
+                                       len(work), ctypes.byref(plan))
+    assert rc == oa.OK
+    return plan, work.reshape(-1, 4)
+
+
+def test_prefill_plan_tiles_cover_every_row_once():
+    r = W.ragged_prefill_case(5, 32, 8, 1, 300, 0, 100, seed=4)
+    plan, work = _plan_host(r.rows, 32, 8, r.seq, r.pos)
+    per_tile = 128 // 4
+    covered = np.zeros(r.rows, int)
+    for s, first, n, _ in work:
+        assert 1 <= n <= per_tile
+        assert np.all(r.seq[first:first + n] == s)
+        assert np.all(np.diff(r.pos[first:first + n]) == 1)
+        covered[first:first + n] += 1
+    assert np.all(covered == 1) and plan.tiles == len(work)
+
+
+def test_prefill_plan_breaks_runs_at_position_gaps():
+    seq = np.array([0, 0, 0, 1, 1, 0, 0], np.int32)
+    pos = np.array([5, 6, 8, 0, 1, 9, 10], np.int32)
+    _, work = _plan_host(7, 4, 4, seq, pos)
+    assert [tuple(w[:3]) for w in work] == [(0, 0, 2), (0, 2, 1), (1, 3, 2), (0, 5, 2)]

@@ -1,0 +1,166 @@
+"""Paged decode on the GPU against the CPU oracle (qwen3_attend / lm_attend
+semantics), plus the bit-exact page-table properties."""
+import numpy as np
+import pytest
+import torch
+
+import omni_attn as oa
+import workloads as W
+from gpu_util import DevPaged, assert_close, dev_i32, host_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_out(oracle, c, threads=8):
+    return oracle.paged_attend(c.qkv, c.kv, c.pos, c.seq, c.ragged, c.indptr, c.pages, c.page, c.hq, c.hk, c.scale,
+                               context=c.context, nthreads=threads)
+
+
+@pytest.mark.parametrize("chunk", [0, 128, 256])
+def test_config1_parity(oracle, chunk):
+    c = W.config_case(1)
+    got = DevPaged(c).decode(chunk=chunk)
+    assert_close(got, oracle_out(oracle, c), what=f"config1 chunk={chunk}")
+
+
+@pytest.mark.parametrize("hq,hk", [(4, 4), (8, 4), (16, 4), (32, 32)])
+@pytest.mark.parametrize("lo,hi", [(1, 40), (1, 1), (500, 1300)])
+def test_head_shapes_and_lengths(oracle, hq, hk, lo, hi):
+    c = W.paged_decode_case(7, hq, hk, lo, hi, seed=hq + hk + lo, slack_pages=3)
+    got = DevPaged(c).decode(chunk=128)
+    assert_close(got, oracle_out(oracle, c), what=f"{hq}/{hk} len[{lo},{hi}]")
+
+
+def test_single_key_rows_are_exact(oracle):
+    c = W.paged_decode_case(6, 8, 4, 1, 1, seed=3)
+    assert np.array_equal(DevPaged(c).decode(), oracle_out(oracle, c))
+
+
+def test_ragged_rows(oracle):
+    c = W.ragged_prefill_case(4, 16, 8, 1, 70, 0, 600, seed=11)
+    got = DevPaged(c).decode(chunk=128)
+    assert_close(got, oracle_out(oracle, c), what="ragged")
+
+
+def test_lm_ring_cap(oracle):
+    c = W.paged_decode_case(9, 8, 8, 100, 3000, seed=12, context=700)
+    past = c.pos + 1 >= 700  # rows whose pages already hold a full ring move past it
+    c.pos = np.where(past, c.pos + np.random.default_rng(1).integers(0, 5000, c.rows), c.pos).astype(np.int32)
+    got = DevPaged(c).decode(lm=True, max_len=700)
+    assert_close(got, oracle_out(oracle, c), what="ring")
+
+
+def test_rows_longer_than_plan_bound(oracle):
+    c = W.paged_decode_case(5, 8, 4, 600, 900, seed=13)
+    got = DevPaged(c).decode(chunk=128, max_len=256)  # the last split absorbs the overflow
+    assert_close(got, oracle_out(oracle, c), what="overflow")
+
+
+def test_lastlen_encoding_is_identical():
+    c = W.paged_decode_case(8, 16, 8, 1, 500, seed=14)
+    d = DevPaged(c)
+    a = d.decode(chunk=128)
+    last = ((c.pos % 16) + 1).astype(np.int32)
+    plan = oa.decode_plan(c.rows, 16, 8, 16, int(c.lens().max()), 128)
+    ws = oa.workspace_for(plan)
+    d.out.zero_()
+    oa.decode_lastlen(d.qkv, d.kv, dev_i32(last), d.seq, 0, d.indptr, d.pages, 16, d.out, 16, 8, c.scale, plan, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(d.out), a)
+
+
+def test_gather_bit_exact(oracle):
+    c = W.paged_decode_case(6, 8, 4, 1, 700, seed=15, slack_pages=5)
+    d = DevPaged(c)
+    lens = c.lens().astype(np.int32)
+    ids = np.array([3, 0, 5, 1], np.int32)
+    sel = lens[ids]
+    out_indptr = np.concatenate([[0], np.cumsum(sel)]).astype(np.int32)
+    out = torch.zeros(int(out_indptr[-1]), 2 * c.hk * 128, dtype=torch.bfloat16, device="cuda")
+    oa.gather_kv(d.kv, c.hk, d.indptr, d.pages, 16, dev_i32(ids), dev_i32(sel), dev_i32(out_indptr), out)
+    torch.cuda.synchronize()
+    got = host_bits(out)
+    for j, s in enumerate(ids):
+        want = oracle.gather_kv(c.kv, c.hk, c.indptr, c.pages, 16, int(s), int(sel[j]))
+        assert np.array_equal(got[out_indptr[j]:out_indptr[j + 1]], want)
+
+
+def test_page_permutation_is_bit_identical():
+    c = W.paged_decode_case(6, 16, 8, 50, 900, seed=16, slack_pages=9)
+    a = DevPaged(c).decode(chunk=256)
+    perm = np.random.default_rng(2).permutation(c.num_pages).astype(np.int32)
+    kv2 = np.empty_like(c.kv)
+    src = c.kv.reshape(c.num_pages, 16, -1)
+    kv2.reshape(c.num_pages, 16, -1)[perm] = src
+    c.kv, c.pages = kv2, perm[c.pages].copy()
+    assert np.array_equal(DevPaged(c).decode(chunk=256), a)
+
+
+def test_row_output_independent_of_neighbours():
+    c = W.paged_decode_case(8, 8, 4, 10, 900, seed=17)
+    a = DevPaged(c).decode(chunk=128, max_len=900)
+    c2 = W.paged_decode_case(8, 8, 4, 10, 900, seed=18)
+    # Row 3 keeps its query, pages and K/V; every other row changes.
+    c2.kv = np.concatenate([c2.kv, c.kv])
+    off = c2.num_pages
+    s = 3
+    n3 = c.indptr[s + 1] - c.indptr[s]
+    pages3 = c.pages[c.indptr[s]:c.indptr[s + 1]] + off
+    pages = np.concatenate([c2.pages[: c2.indptr[s]], pages3, c2.pages[c2.indptr[s + 1]:]]).astype(np.int32)
+    indptr = c2.indptr.copy()
+    indptr[s + 1:] += n3 - (c2.indptr[s + 1] - c2.indptr[s])
+    c2.pages, c2.indptr, c2.num_pages = pages, indptr, c2.num_pages + c.num_pages
+    c2.pos[s] = c.pos[s]
+    c2.qkv[s] = c.qkv[s]
+    b = DevPaged(c2).decode(chunk=128, max_len=900)
+    assert np.array_equal(a[s], b[s])
+
+
+def test_graph_replay_with_new_lengths(oracle):
+    c = W.paged_decode_case(16, 16, 8, 10, 1200, seed=19)
+    d = DevPaged(c)
+    plan = oa.decode_plan(c.rows, 16, 8, 16, 1200, 128)
+    ws = oa.workspace_for(plan)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        oa.qwen3_attend(d.qkv, d.kv, d.pos, d.seq, 0, d.indptr, d.pages, 16, d.out, 16, 8, c.scale, plan, ws, s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        oa.qwen3_attend(d.qkv, d.kv, d.pos, d.seq, 0, d.indptr, d.pages, 16, d.out, 16, 8, c.scale, plan, ws, s)
+    rng = np.random.default_rng(5)
+    for rep in range(4):
+        # New positions inside each row's pages; same buffers.
+        cap = (c.indptr[1:] - c.indptr[:-1]) * 16
+        c.pos = np.minimum(rng.integers(0, 1200, c.rows), cap - 1).astype(np.int32)
+        d.pos.copy_(dev_i32(c.pos))
+        d.out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(host_bits(d.out), oracle_out(oracle, c), what=f"replay {rep}")
+
+
+def _device_values(c, seed):
+    """Full-size values drawn on the device, copied back for the oracle."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    qkv = torch.randn(c.rows, (c.hq + 2 * c.hk) * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    kv = torch.randn(c.num_pages * c.page, 2 * c.hk * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    c.qkv, c.kv = host_bits(qkv), host_bits(kv)
+    return qkv, kv
+
+
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_full_config_parity(oracle, cfg):
+    c = W.config_case(cfg, values=None)
+    qkv, kv = _device_values(c, cfg)
+    d = DevPaged.__new__(DevPaged)
+    d.c, d.qkv, d.kv = c, qkv, kv
+    d.pos, d.seq, d.indptr, d.pages = dev_i32(c.pos), dev_i32(c.seq), dev_i32(c.indptr), dev_i32(c.pages)
+    d.out = torch.zeros(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    max_len = W.CONFIGS[cfg]["len_hi"]
+    got = d.decode(max_len=max_len, lm=cfg == 3)
+    want = oracle_out(oracle, c, threads=16)
+    assert_close(got, want, what=f"config{cfg}")
