@@ -119,10 +119,11 @@ def time_steps(run_step, steps, warmup, stream, per_launch=None):
     return ms, launch_ms
 
 
-def cpu_decode_baseline(cfg=3, rows=16, threads=None):
-    """The oracle (a C port of the reference math) on a bounded sample of the
-    decode workload on this host's cores: the first `rows` sessions of one
-    layer. Returns (GB/s, seconds, threads, description)."""
+def cpu_decode_baseline(cfg=3, rows=32, min_seconds=10.0, threads=None):
+    """The oracle (a C port of the reference math) timed on this host's cores on
+    a bounded sample of the decode workload: the first `rows` sessions of one
+    layer (their pages compacted into a pool of exactly that size), repeated
+    for at least `min_seconds`. Returns (GB/s, seconds per rep, threads, text)."""
     import numpy as np
 
     import oracle
@@ -130,20 +131,18 @@ def cpu_decode_baseline(cfg=3, rows=16, threads=None):
 
     threads = threads or min(16, os.cpu_count() or 1)
     c = W.config_case(cfg, values=None)
-    keep = rows
-    c.pos = c.pos[:keep].copy()
-    c.seq = c.seq[:keep].copy()
-    used = int(c.indptr[keep])
-    c.indptr = c.indptr[: keep + 1].copy()
-    # Compact the pool to the pages these rows use.
-    pages = c.pages[:used]
-    remap = np.arange(used, dtype=np.int32)
+    c.pos, c.seq = c.pos[:rows].copy(), c.seq[:rows].copy()
+    used = int(c.indptr[rows])
+    c.indptr = c.indptr[: rows + 1].copy()
     rng = np.random.default_rng(7)
-    c.qkv = oracle.normal_bf16(keep * (c.hq + 2 * c.hk) * 128, 11).reshape(keep, -1)
-    c.kv = oracle.normal_bf16(used * c.page * 2 * c.hk * 128, 12).reshape(used * c.page, -1)
-    c.pages = rng.permutation(remap).astype(np.int32)
-    del pages
+    c.pages = rng.permutation(used).astype(np.int32)
     c.num_pages = used
+
+    def values(n):  # normal bf16 in +-[1/8, 2) with random sign and mantissa: timing only
+        return (rng.integers(0, 1 << 16, n, dtype=np.uint16) & np.uint16(0x81FF)) | np.uint16(0x3E00)
+
+    c.qkv = values(rows * (c.hq + 2 * c.hk) * 128).reshape(rows, -1)
+    c.kv = values(used * c.page * 2 * c.hk * 128).reshape(used * c.page, -1)
     args = (c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, c.page, c.hq, c.hk, c.scale)
     oracle.paged_attend(*args, context=c.context, nthreads=threads)  # warm
     reps, t0 = 0, time.perf_counter()
@@ -151,10 +150,94 @@ def cpu_decode_baseline(cfg=3, rows=16, threads=None):
         oracle.paged_attend(*args, context=c.context, nthreads=threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 5:
+        if el >= min_seconds:
             break
     sec = el / reps
-    return c.kv_bytes() / sec / 1e9, sec, threads, f"config{cfg}, first {keep} of {W.CONFIGS[cfg]['rows']} sessions, 1 layer, median-free mean of {reps} reps"
+    text = (f"config{cfg}: first {rows} of {W.CONFIGS[cfg]['rows']} sessions of one layer "
+            f"({c.kv_bytes() / 1e9:.3f} GB algorithmic), {reps} reps over {el:.1f} s")
+    return c.kv_bytes() / sec / 1e9, sec, threads, text
+
+
+def prefill_bench(stream, steps, warmup):
+    """Config 4: one ragged causal prefill launch over paged K/V per step."""
+    import numpy as np
+    import torch
+
+    import omni_attn as oa
+    import workloads as W
+
+    c = W.config_case(4, values=None)
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    qkv = torch.empty(c.rows, (c.hq + 2 * c.hk) * 128, dtype=torch.bfloat16, device="cuda").normal_(generator=gen)
+    kv = torch.empty(c.num_pages * c.page, 2 * c.hk * 128, dtype=torch.bfloat16, device="cuda").normal_(generator=gen)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+    pos, seq, indptr, pages = i32(c.pos), i32(c.seq), i32(c.indptr), i32(c.pages)
+    out = torch.empty(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    pf = oa.prefill_plan(c.rows, c.hq, c.hk, c.page, c.seq, c.pos)
+
+    def step(s, ev):
+        if ev is not None:
+            ev[0][0].record(s)
+        oa.prefill_run(pf, qkv, kv, pos, seq, indptr, pages, out, c.scale, s)
+        if ev is not None:
+            ev[0][1].record(s)
+
+    ms, launch_ms = time_steps(step, steps, warmup, stream, per_launch=1)
+    fl = W.prefill_flops(c)
+    return dict(workload="config4: " + W.CONFIGS[4]["desc"], rows=c.rows, flops=fl, ms_per_step=round(ms, 4),
+                tflops=round(fl / (ms * 1e-3) / 1e12, 2), launch_us=round(launch_ms * 1e3, 2),
+                frac=round(fl / (launch_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
+
+
+def dit_bench(stream, steps, warmup, hk=8):
+    """Config 5: the HiDream CFG pair's full attention, one launch per step."""
+    import numpy as np
+    import torch
+
+    import omni_attn as oa
+    import workloads as W
+
+    cfg = W.CONFIGS[5]
+    c = W.dense_case(cfg["hq"], hk, cfg["q_len"], cfg["kv_len"], 0, batch=cfg["batch"], values=None)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+
+    def rms(x):
+        x = x.view(*x.shape[:-1], -1, 128)
+        return (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)).view(*x.shape[:-2], -1)
+
+    q = rms(torch.randn(c.batch, c.q_len, c.q_stride, device="cuda", generator=gen)).to(torch.bfloat16)
+    k = rms(torch.randn(c.batch, c.kv_len, hk * 128, device="cuda", generator=gen)).to(torch.bfloat16)
+    v = torch.randn(c.batch, c.kv_len, hk * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    out = torch.empty(c.batch, c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    kvl = torch.tensor([c.kv_len], dtype=torch.int32, device="cuda")
+
+    def step(s, ev):
+        if ev is not None:
+            ev[0][0].record(s)
+        oa.hidream_attend_batched(q, k, v, out, c.q_len, kvl, c.q_stride, 0, c.scale_log2, c.hq, hk, c.batch,
+                                  c.q_len * c.q_stride, c.kv_len * hk * 128, c.q_len * c.hq * 128, s)
+        if ev is not None:
+            ev[0][1].record(s)
+
+    ms, launch_ms = time_steps(step, steps, warmup, stream, per_launch=1)
+    fl = c.flops()
+    return dict(workload=f"config5: {W.CONFIGS[5]['desc']} (hk={hk})", flops=fl, ms_per_step=round(ms, 4),
+                tflops=round(fl / (ms * 1e-3) / 1e12, 2), launch_us=round(launch_ms * 1e3, 2),
+                frac=round(fl / (launch_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
+
+
+def copy_calibration(mb):
+    """A plain device copy of `mb` MiB, 5 times: the known-size kernel that
+    scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    a = torch.empty(mb << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_mib": mb, "bytes_read": mb << 20, "bytes_written": mb << 20}))
 
 
 def main():
@@ -165,8 +248,12 @@ def main():
     ap.add_argument("--pools", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", type=int, default=0, help="run one config (2, 3, 4 or 5) and report it")
+    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     args = ap.parse_args()
+    if args.calib_copy_mib:
+        copy_calibration(args.calib_copy_mib)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -178,7 +265,33 @@ def main():
     stream = torch.cuda.Stream()
     extra = {}
 
-    cfg = args.only if args.only in (2, 3) else 3
+    if args.only in (0, 4):
+        log("[bench] config 4 prefill")
+        extra["config4"] = prefill_bench(stream, args.steps, args.warmup)
+        log(f"[bench] {extra['config4']}")
+    if args.only in (0, 5):
+        log("[bench] config 5 DiT")
+        extra["config5"] = dit_bench(stream, args.steps, args.warmup)
+        log(f"[bench] {extra['config5']}")
+        if args.only == 0:
+            extra["config5_mha"] = dit_bench(stream, args.steps, args.warmup, hk=32)
+    if args.only in (0, 2):
+        log("[bench] config 2 decode")
+        b2 = DecodeBench(2, args.pools, chunk=args.chunk)
+        ms2, l2 = time_steps(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream, per_launch=b2.layers)
+        tb = sum(b2.bytes_per_layer)
+        extra["config2"] = dict(workload="config2: " + __import__("workloads").CONFIGS[2]["desc"],
+                                ms_per_step=round(ms2, 4), gbs=round(tb / (ms2 * 1e-3) / 1e9, 1),
+                                launch_us=round(l2 * 1e3, 2), chunk=b2.plan.chunk,
+                                frac=round(tb / b2.layers / (l2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        log(f"[bench] {extra['config2']}")
+        del b2
+        torch.cuda.empty_cache()
+    if args.only in (4, 5, 2):
+        print(json.dumps({"extra": extra}), flush=True)
+        return
+
+    cfg = 3
     log(f"[bench] decode config {cfg}: building workload")
     b = DecodeBench(cfg, args.pools, chunk=args.chunk)
     log(f"[bench] decode config {cfg}: plan chunk={b.plan.chunk} splits={b.plan.splits}; timing")
@@ -193,6 +306,7 @@ def main():
     if not args.no_cpu:
         log("[bench] cpu baseline (oracle port)")
         v, sec, thr, sample = cpu_decode_baseline(cfg)
+        log(f"[bench] cpu: {v:.2f} GB/s on {thr} threads")
         cpu = {"value": round(v, 3), "unit": "GB/s", "cores": thr, "kind": "port", "sample": sample,
                "seconds_per_sample": round(sec, 4)}
 

@@ -1,6 +1,329 @@
+// Tiled flash attention on bf16 MFMA (gfx950) for the ragged causal prefill
+// over the paged cache and the HiDream-O1 DiT attention over dense K/V.
+//
+// Semantics: prefill rows are qwen3_attend(ragged = 1) rows
+// (crates/omni-qwen3/kernels/qwen3.cu:234-240): row n sees keys 0..pos[n] of
+// sequence seq[n]. DiT rows are hidream_attend rows (crates/omni-hidream-o1/
+// kernels/hidream.cu:209-347): row n sees the first *kv_len_at keys, with
+// `causal` only keys 0..n; softmax in base 2 with P rounded to bf16 for P.V.
+//
+// A workgroup (4 waves) owns 128 packed query rows: (128 / G positions) x (the
+// G query heads of one K/V head), so one K/V tile in LDS serves G heads. Wave w
+// owns packed rows 32w..32w+31. Keys stream through LDS 64 at a time, double
+// buffered: global loads of tile s+1 are in flight while tile s is computed.
+//
+// Per wave and key tile, on v_mfma_f32_32x32x16_bf16:
+//   S^T (64 keys x 32 rows) = K (64 x 128) . Q^T (128 x 32): 2 x 8 MFMAs,
+//     K from LDS as the A operand, Q held in registers as the B operand.
+//     In the 32x32 accumulator a lane holds one query column (lane % 32) and 16
+//     keys, so the row max and sum are lane-local plus one exchange with lane ^ 32.
+//   O^T (128 dims x 32 rows) += V^T (128 x 64) . P^T (64 x 32): 4 x 4 MFMAs.
+//     P^T's B operand is the S accumulator itself (rounded to bf16): lane half h
+//     of K-step ks holds keys 16 ks + 4 h + {0..3, 8..11}, and V^T is read from
+//     LDS at exactly those keys. V is stored transposed in LDS ([dim][key]).
+// LDS swizzles keep every ds_read / ds_write conflict-free (see k_off, vt_off).
 #include "common.h"
 #include "kernels.h"
+
 namespace omni {
-int launch_prefill(const TiledArgs&, int, hipStream_t) { return -2; }
-int launch_dit(const TiledArgs&, int, hipStream_t) { return -2; }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = kTiledRows;  // packed query rows per workgroup
+constexpr int kBN = 64;          // keys per tile
+constexpr int kThreads = 256;
+constexpr int kTileElems = kBN * kHead;  // bf16 elements of one K (or V^T) tile
+
+// K tile, row-major [key][128]: 16-byte chunk c of key row r sits at chunk
+// c ^ (r & 7), so 8 consecutive keys' same chunk hit 8 different bank groups.
+__device__ __forceinline__ int k_off(int key, int chunk) { return key * kHead + ((chunk ^ (key & 7)) << 3); }
+
+// V^T tile, [dim][64 keys]: 8-byte granule g (4 keys) of dim row d sits at
+// g ^ (((d >> 3) ^ d) & 15). Reads (16 consecutive d, one granule) and the
+// transposing writes (d = 8c + i for 16 values of c) both spread over 16
+// different granules.
+__device__ __forceinline__ int vt_off(int d, int granule) {
+  return d * kBN + ((granule ^ (((d >> 3) ^ d) & 15)) << 2);
 }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Pack 8 f32 to 8 bf16 (RNE) as an MFMA operand.
+__device__ __forceinline__ bf16x8 pack8(const float* v) {
+  uint4 u;
+  u.x = pack_bf16x2(v[0], v[1]);
+  u.y = pack_bf16x2(v[2], v[3]);
+  u.z = pack_bf16x2(v[4], v[5]);
+  u.w = pack_bf16x2(v[6], v[7]);
+  return as_bf16x8(u);
+}
+
+struct Tile {
+  const bf16_t* q;    // row p of the tile at q + p * q_stride (head offset added per row)
+  bf16_t* out;        // row p at out + p * hq * 128
+  int nq;             // positions in the tile (<= 128 / G)
+  int len;            // keys of the source
+  int last;           // keys any row of the tile sees
+  int qpos0;          // DiT: position of row 0 (causal rule n sees 0..n)
+  const int32_t* pos; // prefill: positions of the tile's rows
+  // key sources
+  const bf16_t* kbase;
+  const bf16_t* vbase;
+  int64_t kv_stride;         // dense: elements between keys
+  const int32_t* pg;         // paged: the sequence's pages
+  int64_t per_slot;          // paged: elements per slot
+};
+
+template <int G, bool PAGED>
+__global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items, int ntiles) {
+  // XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
+  // contiguous block of work items so the tiles sharing one K/V head (and
+  // batch) share that XCD's L2.
+  const int per = (items + 7) >> 3;
+  const int idx = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (idx >= items) return;
+  const int tile = idx % ntiles;
+  const int kvh = (idx / ntiles) % a.hk;
+  const int b = idx / (ntiles * a.hk);
+  constexpr int kPos = kBM / G;  // positions per tile
+
+  Tile t;
+  if constexpr (PAGED) {
+    const int s = a.work[tile * 4 + 0], first = a.work[tile * 4 + 1];
+    t.nq = a.work[tile * 4 + 2];
+    t.pos = a.pos + first;
+    t.q = a.q + (int64_t)first * a.q_stride;
+    t.out = a.out + (int64_t)first * a.hq * kHead;
+    t.last = t.pos[t.nq - 1] + 1;
+    t.len = t.last;
+    t.pg = a.pages + a.indptr[s];
+    t.per_slot = 2LL * a.hk * kHead;
+    t.kbase = a.kv + (int64_t)kvh * kHead;
+    t.vbase = a.kv + (int64_t)(a.hk + kvh) * kHead;
+    t.qpos0 = 0;
+  } else {
+    const int q0 = tile * kPos;
+    t.nq = min(kPos, a.q_len - q0);
+    t.q = a.q + b * a.q_bstride + (int64_t)q0 * a.q_stride;
+    t.out = a.out + b * a.out_bstride + (int64_t)q0 * a.hq * kHead;
+    t.len = *a.kv_len_at;
+    t.last = a.causal ? min(t.len, q0 + t.nq) : t.len;
+    t.qpos0 = q0;
+    t.kv_stride = (int64_t)a.hk * kHead;
+    t.kbase = a.k + b * a.kv_bstride + (int64_t)kvh * kHead;
+    t.vbase = a.v + b * a.kv_bstride + (int64_t)kvh * kHead;
+  }
+
+  // Buffer i: K tile at smem + 2 i tiles, V^T tile right after it.
+  __shared__ __align__(16) bf16_t smem[4 * kTileElems];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = lane & 31, h = lane >> 5;
+
+  // This lane's query column: packed row r = 32 wave + j.
+  const int r = wave * 32 + j;
+  const int p = r / G, head = kvh * G + r % G;
+  const bool row_ok = p < t.nq;
+  int lim;  // keys this row sees
+  if constexpr (PAGED)
+    lim = row_ok ? t.pos[p] + 1 : 0;
+  else
+    lim = row_ok ? (a.causal ? min(t.len, t.qpos0 + p + 1) : t.len) : 0;
+
+  // Q^T as the B operand: K-step kk holds dims 16 kk + 8 h .. + 7 of row r.
+  bf16x8 qf[8];
+  {
+    const bf16_t* qp = t.q + (int64_t)(row_ok ? p : 0) * a.q_stride + (int64_t)head * kHead + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      uint4 u = row_ok ? ldg16(qp + 16 * kk) : make_uint4(0, 0, 0, 0);
+      qf[kk] = as_bf16x8(u);
+    }
+  }
+
+  // Loader role: keys 4 kg + u (u < 4) of a tile, 16-byte chunk c.
+  const int kg = tid >> 4, lc = tid & 15;
+  uint4 kr[4], vr[4];
+  auto load_tile = [&](int n0) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int key = min(n0 + 4 * kg + u, t.last - 1);
+      int64_t ko, vo;
+      if constexpr (PAGED) {
+        const int sh = a.page_shift;
+        const int64_t slot = ((int64_t)t.pg[key >> sh] << sh) | (key & ((1 << sh) - 1));
+        ko = vo = slot * t.per_slot + lc * 8;
+      } else {
+        ko = vo = (int64_t)key * t.kv_stride + lc * 8;
+      }
+      kr[u] = ldg16(t.kbase + ko);
+      vr[u] = ldg16(t.vbase + vo);
+    }
+  };
+  auto store_tile = [&](int buf) {
+    bf16_t* kd = smem + 2 * buf * kTileElems;
+    bf16_t* vd = kd + kTileElems;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(kd + k_off(4 * kg + u, lc)) = kr[u];
+    // Transpose 4 keys x 8 dims into 8 dim rows of 4 keys (8 bytes each).
+    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vr[0]);
+    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vr[1]);
+    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&vr[2]);
+    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&vr[3]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int w = i >> 1;
+      uint2 o;
+      if (i & 1) {
+        o.x = (w0[w] >> 16) | (w1[w] & 0xffff0000u);
+        o.y = (w2[w] >> 16) | (w3[w] & 0xffff0000u);
+      } else {
+        o.x = (w0[w] & 0xffffu) | (w1[w] << 16);
+        o.y = (w2[w] & 0xffffu) | (w3[w] << 16);
+      }
+      *reinterpret_cast<uint2*>(vd + vt_off(8 * lc + i, kg)) = o;
+    }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int md = 0; md < 4; ++md)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[md][e] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  const float sl2 = a.scale_log2;
+
+  const int steps = (t.last + kBN - 1) / kBN;
+  if (steps > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < steps; ++st) {
+    const int buf = st & 1;
+    const int n0 = st * kBN;
+    if (st + 1 < steps) load_tile(n0 + kBN);
+    const bf16_t* kt = smem + 2 * buf * kTileElems;
+    const bf16_t* vt = kt + kTileElems;
+
+    // S^T = K . Q^T for keys n0 .. n0 + 63.
+    f32x16 sc[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[mb][e] = 0.f;
+      const int key = 32 * mb + j;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(kt + k_off(key, 2 * kk + h)));
+        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[mb], 0, 0, 0);
+      }
+    }
+    // Register e of block mb is key n0 + 32 mb + 8 (e / 4) + 4 h + e % 4.
+    if (__any(n0 + kBN > lim)) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (n0 + 32 * mb + 8 * (e >> 2) + 4 * h + (e & 3) >= lim) sc[mb][e] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[mb][e]);
+    mx = fmaxf(mx, xor_lane(mx, 32));
+    const float m_new = fmaxf(m, mx * sl2);
+    const float base = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m - base);
+    m = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sc[mb][e] = fast_exp2(fmaf(sc[mb][e], sl2, -base));
+        psum += sc[mb][e];
+      }
+    l = fmaf(l, alpha, psum);
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[md][e] *= alpha;
+
+    // O^T += V^T . P^T: K-step ks covers keys 16 ks + 4 h + {0..3, 8..11}.
+#pragma unroll
+    for (int ks_ = 0; ks_ < 4; ++ks_) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = sc[ks_ >> 1][8 * (ks_ & 1) + e];
+      const bf16x8 pf = pack8(pv);
+      const int g0 = 4 * ks_ + h, g1 = 4 * ks_ + 2 + h;  // granules of keys 16ks+4h.. and 16ks+8+4h..
+#pragma unroll
+      for (int md = 0; md < 4; ++md) {
+        const int d = 32 * md + j;
+        uint4 u;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vt + vt_off(d, g0));
+        const uint2 hi = *reinterpret_cast<const uint2*>(vt + vt_off(d, g1));
+        u.x = lo.x;
+        u.y = lo.y;
+        u.z = hi.x;
+        u.w = hi.y;
+        o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u), pf, o[md], 0, 0, 0);
+      }
+    }
+    if (st + 1 < steps) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Normalise and store: register e of block md is dim 32 md + 8 (e / 4) + 4 h + e % 4.
+  l += xor_lane(l, 32);
+  if (!row_ok) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  bf16_t* dst = t.out + ((int64_t)p * a.hq + head) * kHead;
+#pragma unroll
+  for (int md = 0; md < 4; ++md)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = 32 * md + 8 * q4 + 4 * h;
+      uint2 w;
+      w.x = pack_bf16x2(o[md][4 * q4 + 0] * inv, o[md][4 * q4 + 1] * inv);
+      w.y = pack_bf16x2(o[md][4 * q4 + 2] * inv, o[md][4 * q4 + 3] * inv);
+      *reinterpret_cast<uint2*>(dst + d) = w;
+    }
+}
+
+template <bool PAGED>
+int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) {
+  if (items <= 0) return 0;
+  const int grid = ((items + 7) >> 3) << 3;
+  switch (a.hq / a.hk) {
+#define OMNI_CASE(G)                                                                       \
+  case G:                                                                                  \
+    tiled_attn<G, PAGED><<<grid, kThreads, 0, stream>>>(a, items, ntiles);       \
+    break;
+    OMNI_CASE(1)
+    OMNI_CASE(2)
+    OMNI_CASE(4)
+    OMNI_CASE(8)
+#undef OMNI_CASE
+    default: return -2;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream) {
+  return launch_tiled<true>(a, tiles * a.hk, tiles, stream);
+}
+
+int launch_dit(const TiledArgs& a, int batch, hipStream_t stream) {
+  const int G = a.hq / a.hk;
+  if (G <= 0 || kBM % G != 0) return -2;
+  const int ntiles = (a.q_len + kBM / G - 1) / (kBM / G);
+  const long long items = (long long)ntiles * a.hk * batch;
+  if (items > (1LL << 30)) return -2;
+  return launch_tiled<false>(a, (int)items, ntiles, stream);
+}
+
+}  // namespace omni

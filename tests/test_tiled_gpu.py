@@ -1,0 +1,108 @@
+"""MFMA prefill (ragged causal over the paged cache) and HiDream DiT
+attention on the GPU against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+import omni_attn as oa
+import workloads as W
+from gpu_util import assert_close, dev_bits, dev_i32, host_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(c):
+    pf = oa.prefill_plan(c.rows, c.hq, c.hk, c.page, c.seq, c.pos)
+    out = torch.zeros(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    oa.prefill_run(pf, dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), dev_i32(c.indptr),
+                   dev_i32(c.pages), out, c.scale)
+    torch.cuda.synchronize()
+    return host_bits(out)
+
+
+def oracle_paged(oracle, c, threads=16):
+    return oracle.paged_attend(c.qkv, c.kv, c.pos, c.seq, c.ragged, c.indptr, c.pages, c.page, c.hq, c.hk, c.scale,
+                               nthreads=threads)
+
+
+@pytest.mark.parametrize("hq,hk", [(32, 8), (16, 16), (16, 8), (64, 8)])
+def test_prefill_parity(oracle, hq, hk):
+    c = W.ragged_prefill_case(3, hq, hk, 1, 300, 0, 200, seed=hq + hk)
+    assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill {hq}/{hk}")
+
+
+def test_prefill_single_rows_and_odd_lengths(oracle):
+    c = W.ragged_prefill_case(6, 32, 8, 1, 3, 0, 70, seed=3)
+    assert_close(run_prefill(c), oracle_paged(oracle, c), what="short")
+
+
+def test_prefill_matches_decode_kernel(oracle):
+    """The same rows through the split-K decode kernel: two kernels, one answer."""
+    c = W.ragged_prefill_case(4, 32, 8, 50, 200, 0, 300, seed=4)
+    a = run_prefill(c)
+    plan = oa.decode_plan(c.rows, 32, 8, 16, int(c.pos.max()) + 1, 128)
+    out = torch.zeros(c.rows, 32 * 128, dtype=torch.bfloat16, device="cuda")
+    oa.qwen3_attend(dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), 1, dev_i32(c.indptr),
+                    dev_i32(c.pages), 16, out, 32, 8, c.scale, plan, oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    assert_close(a, host_bits(out), what="prefill vs decode")
+
+
+def test_prefill_config4_subset(oracle):
+    """Config 4's construction (new U[512,4096], cached U[0,1024]) on 2 requests."""
+    c = W.ragged_prefill_case(2, 32, 8, 512, 4096, 0, 1024, seed=4000)
+    assert_close(run_prefill(c), oracle_paged(oracle, c), what="config4 subset")
+
+
+def run_dense(c, b_all=True):
+    q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
+    out = torch.zeros(c.batch, c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    kvl = dev_i32(np.array([c.kv_len], np.int32))
+    if c.batch == 1:
+        oa.hidream_attend(q, k, v, out, c.q_len, kvl, c.q_stride, c.causal, c.scale_log2, c.hq, c.hk)
+    else:
+        oa.hidream_attend_batched(q, k, v, out, c.q_len, kvl, c.q_stride, c.causal, c.scale_log2, c.hq, c.hk, c.batch,
+                                  c.q_len * c.q_stride, c.kv_len * c.hk * 128, c.q_len * c.hq * 128)
+    torch.cuda.synchronize()
+    return host_bits(out)
+
+
+def oracle_dense(oracle, c, b=0, kv_len=None):
+    return oracle.dense_attend(np.ascontiguousarray(c.q[b]), np.ascontiguousarray(c.k[b]),
+                               np.ascontiguousarray(c.v[b]), c.q_len, kv_len or c.kv_len, c.q_stride, c.hq, c.hk,
+                               c.causal, c.scale_log2, nthreads=16)
+
+
+@pytest.mark.parametrize("hq,hk,q_len,kv_len,causal", [
+    (32, 8, 300, 300, 1), (32, 8, 257, 333, 0), (8, 8, 100, 130, 0), (4, 4, 1, 1, 0), (16, 8, 65, 64, 1),
+    (32, 4, 40, 500, 0),
+])
+def test_dit_parity(oracle, hq, hk, q_len, kv_len, causal):
+    c = W.dense_case(hq, hk, q_len, kv_len, causal, seed=q_len)
+    assert_close(run_dense(c)[0], oracle_dense(oracle, c), what=f"dit {hq}/{hk} {q_len}x{kv_len} c{causal}")
+
+
+def test_dit_kv_len_read_from_device(oracle):
+    c = W.dense_case(32, 8, 200, 400, 0, seed=7)
+    q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
+    out = torch.zeros(c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    kvl = dev_i32(np.array([259], np.int32))
+    oa.hidream_attend(q, k, v, out, c.q_len, kvl, c.q_stride, 0, c.scale_log2, c.hq, c.hk)
+    torch.cuda.synchronize()
+    assert_close(host_bits(out), oracle_dense(oracle, c, kv_len=259), what="kv_len 259")
+
+
+def test_dit_batched_pair(oracle):
+    c = W.dense_case(32, 8, 130, 130, 0, batch=2, seed=8)
+    got = run_dense(c)
+    for b in range(2):
+        assert_close(got[b], oracle_dense(oracle, c, b), what=f"batch {b}")
+
+
+def test_dit_config5_subset(oracle):
+    """Config 5's shape (4352 keys, 32q/8kv, RMS-normed q/k) on the first 256 queries."""
+    c = W.dense_case(32, 8, 4352, 4352, 0, seed=5000)
+    got = run_dense(c)[0]
+    sub = W.DenseCase(hq=32, hk=8, q_len=256, kv_len=4352, causal=0, q_stride=c.q_stride, q=c.q, k=c.k, v=c.v)
+    want = oracle_dense(oracle, sub)
+    assert_close(got[:256], want, what="config5 first 256 rows")
