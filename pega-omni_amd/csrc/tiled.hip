@@ -21,7 +21,7 @@
 //     P^T's B operand is the S accumulator itself (rounded to bf16): lane half h
 //     of K-step ks holds keys 16 ks + 4 h + {0..3, 8..11}, and V^T is read from
 //     LDS at exactly those keys. V is stored transposed in LDS ([dim][key]).
-// LDS swizzles keep every ds_read / ds_write conflict-free (see k_off, vt_off).
+// LDS layouts keep the MFMA operand reads conflict-free (see kKRow, vt_off).
 #include "common.h"
 #include "kernels.h"
 
@@ -33,18 +33,24 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBM = kTiledRows;  // packed query rows per workgroup
 constexpr int kBN = 64;          // keys per tile
 constexpr int kThreads = 256;
-constexpr int kTileElems = kBN * kHead;  // bf16 elements of one K (or V^T) tile
+// LDS per buffer: the K tile row-major with rows padded to 272 bytes, so the
+// 32 rows an A-operand read touches fall in distinct bank groups and every
+// read address is a per-lane base plus a constant; then the V^T tile.
+constexpr int kKRow = kHead + 8;
+constexpr int kKTileElems = kBN * kKRow;
+constexpr int kVTileElems = kHead * kBN;
+constexpr int kBufElems = kKTileElems + kVTileElems;
 
-// K tile, row-major [key][128]: 16-byte chunk c of key row r sits at chunk
-// c ^ (r & 7), so 8 consecutive keys' same chunk hit 8 different bank groups.
-__device__ __forceinline__ int k_off(int key, int chunk) { return key * kHead + ((chunk ^ (key & 7)) << 3); }
-
-// V^T tile, [dim][64 keys]: 8-byte granule g (4 keys) of dim row d sits at
-// g ^ (((d >> 3) ^ d) & 15). Reads (16 consecutive d, one granule) and the
-// transposing writes (d = 8c + i for 16 values of c) both spread over 16
-// different granules.
-__device__ __forceinline__ int vt_off(int d, int granule) {
-  return d * kBN + ((granule ^ (((d >> 3) ^ d) & 15)) << 2);
+// V^T tile, [dim][64 keys], 128-byte rows of eight 16-byte units. The A
+// operand of K-step ks in lane half h needs keys 16 ks + 4 h + {0..3, 8..11}
+// at one dim: those 8 keys form unit 2 ks + h (first 8 bytes keys +0..3,
+// then +8..11), so one ds_read_b128 feeds one MFMA. Units are XOR-swizzled
+// with f(d) = (d ^ (d >> 3)) & 7: eight lanes reading consecutive dims hit
+// eight different units (no conflict); the transposing writes of 16 lanes
+// (dims 8 c + i) pair up two-way.
+__device__ __forceinline__ int vt_off(int d, int granule) {  // granule = 4 keys 4g..4g+3
+  const int unit = ((granule >> 2) << 1) | (granule & 1), half = (granule >> 1) & 1;
+  return d * kBN + 8 * (unit ^ ((d ^ (d >> 3)) & 7)) + 4 * half;
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
@@ -115,8 +121,8 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     t.vbase = a.v + b * a.kv_bstride + (int64_t)kvh * kHead;
   }
 
-  // Buffer i: K tile at smem + 2 i tiles, V^T tile right after it.
-  __shared__ __align__(16) bf16_t smem[4 * kTileElems];
+  // Buffer i: K tile at smem + i * kBufElems, V^T tile right after it.
+  __shared__ __align__(16) bf16_t smem[2 * kBufElems];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
@@ -137,35 +143,49 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     const bf16_t* qp = t.q + (int64_t)(row_ok ? p : 0) * a.q_stride + (int64_t)head * kHead + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-      uint4 u = row_ok ? ldg16(qp + 16 * kk) : make_uint4(0, 0, 0, 0);
+      uint4 u = ldg16(qp + 16 * kk);  // rows past the tile read row 0, then become zero
+      if (!row_ok) u = make_uint4(0, 0, 0, 0);
       qf[kk] = as_bf16x8(u);
     }
+    // Q is loaded once: wait for it here, so the key loop's first MFMA does
+    // not wait on the next tile's prefetch (vmcnt(0), other counters free).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
   }
 
   // Loader role: keys 4 kg + u (u < 4) of a tile, 16-byte chunk c.
   const int kg = tid >> 4, lc = tid & 15;
   uint4 kr[4], vr[4];
   auto load_tile = [&](int n0) {
+    // Keys n0 + 4 kg + u share one page (page >= 4); past `last` they repeat
+    // the last key, whose scores are masked.
+    const int k0 = min(n0 + 4 * kg, t.last - 1);
+    const int room = t.last - 1 - k0;  // keys k0 + u with u <= room exist
+    const bf16_t* kp;
+    const bf16_t* vp;
+    int64_t step;
+    if constexpr (PAGED) {
+      const int sh = a.page_shift;
+      const int64_t slot = ((int64_t)t.pg[k0 >> sh] << sh) | (k0 & ((1 << sh) - 1));
+      kp = t.kbase + slot * t.per_slot + lc * 8;
+      vp = t.vbase + slot * t.per_slot + lc * 8;
+      step = t.per_slot;
+    } else {
+      kp = t.kbase + (int64_t)k0 * t.kv_stride + lc * 8;
+      vp = t.vbase + (int64_t)k0 * t.kv_stride + lc * 8;
+      step = t.kv_stride;
+    }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int key = min(n0 + 4 * kg + u, t.last - 1);
-      int64_t ko, vo;
-      if constexpr (PAGED) {
-        const int sh = a.page_shift;
-        const int64_t slot = ((int64_t)t.pg[key >> sh] << sh) | (key & ((1 << sh) - 1));
-        ko = vo = slot * t.per_slot + lc * 8;
-      } else {
-        ko = vo = (int64_t)key * t.kv_stride + lc * 8;
-      }
-      kr[u] = ldg16(t.kbase + ko);
-      vr[u] = ldg16(t.vbase + vo);
+      const int64_t off = u <= room ? u * step : 0;
+      kr[u] = ldg16(kp + off);
+      vr[u] = ldg16(vp + off);
     }
   };
   auto store_tile = [&](int buf) {
-    bf16_t* kd = smem + 2 * buf * kTileElems;
-    bf16_t* vd = kd + kTileElems;
+    bf16_t* kd = smem + buf * kBufElems;
+    bf16_t* vd = kd + kKTileElems;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(kd + k_off(4 * kg + u, lc)) = kr[u];
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(kd + (4 * kg + u) * kKRow + 8 * lc) = kr[u];
     // Transpose 4 keys x 8 dims into 8 dim rows of 4 keys (8 bytes each).
     const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vr[0]);
     const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vr[1]);
@@ -194,6 +214,13 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   float m = -INFINITY, l = 0.f;
   const float sl2 = a.scale_log2;
 
+  // Per-lane LDS bases: the A operand of S reads K row 32 mb + j at dims
+  // 16 kk + 8 h (base + constant); the A operand of P.V reads V^T row
+  // 32 md + j, unit 2 ks + h, whose swizzle splits into a lane part and a
+  // constant: elem = 2048 md + ((64 j + 8 (h ^ fj)) ^ (16 ks ^ 32 (md & 1))).
+  const int k_lane = j * kKRow + 8 * h;
+  int v_lane = 64 * j + 8 * (h ^ ((j ^ (j >> 3)) & 7));
+
   const int steps = (t.last + kBN - 1) / kBN;
   if (steps > 0) {
     load_tile(0);
@@ -204,22 +231,29 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     const int buf = st & 1;
     const int n0 = st * kBN;
     if (st + 1 < steps) load_tile(n0 + kBN);
-    const bf16_t* kt = smem + 2 * buf * kTileElems;
-    const bf16_t* vt = kt + kTileElems;
+    const bf16_t* kt = smem + buf * kBufElems;
+    const bf16_t* vt = kt + kKTileElems;
+    asm volatile("" : "+v"(v_lane));  // keep the 32 V^T addresses out of registers across the loop
 
-    // S^T = K . Q^T for keys n0 .. n0 + 63.
+    // S^T = K . Q^T for keys n0 .. n0 + 63: all 16 K fragments first, then
+    // two interleaved MFMA chains.
+    uint4 kf[2][8];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk)
+        kf[mb][kk] = *reinterpret_cast<const uint4*>(kt + k_lane + mb * 32 * kKRow + 16 * kk);
     f32x16 sc[2];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[mb][e] = 0.f;
-      const int key = 32 * mb + j;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(kt + k_off(key, 2 * kk + h)));
-        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[mb], 0, 0, 0);
-      }
-    }
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[mb][kk]), qf[kk], sc[mb], 0, 0, 0);
+
     // Register e of block mb is key n0 + 32 mb + 8 (e / 4) + 4 h + e % 4.
     if (__any(n0 + kBN > lim)) {
 #pragma unroll
@@ -234,10 +268,21 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[mb][e]);
     mx = fmaxf(mx, xor_lane(mx, 32));
-    const float m_new = fmaxf(m, mx * sl2);
-    const float base = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m - base);
-    m = m_new;
+    // The running base m moves only when the max grows by more than 8 (log2):
+    // p = 2^(s - m) <= 2^8 stays exact in f32 and l, O share the same base,
+    // so the result is unchanged while most tiles skip rescaling O.
+    const float mt = mx * sl2;
+    const bool grow = mt > m + 8.f;
+    if (__any(grow)) {
+      const float alpha = grow ? fast_exp2(m - mt) : 1.f;
+      m = grow ? mt : m;
+      l *= alpha;
+#pragma unroll
+      for (int md = 0; md < 4; ++md)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[md][e] *= alpha;
+    }
+    const float base = m == -INFINITY ? 0.f : m;
     float psum = 0.f;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -246,11 +291,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
         sc[mb][e] = fast_exp2(fmaf(sc[mb][e], sl2, -base));
         psum += sc[mb][e];
       }
-    l = fmaf(l, alpha, psum);
-#pragma unroll
-    for (int md = 0; md < 4; ++md)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[md][e] *= alpha;
+    l += psum;
 
     // O^T += V^T . P^T: K-step ks covers keys 16 ks + 4 h + {0..3, 8..11}.
 #pragma unroll
@@ -259,17 +300,9 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = sc[ks_ >> 1][8 * (ks_ & 1) + e];
       const bf16x8 pf = pack8(pv);
-      const int g0 = 4 * ks_ + h, g1 = 4 * ks_ + 2 + h;  // granules of keys 16ks+4h.. and 16ks+8+4h..
 #pragma unroll
       for (int md = 0; md < 4; ++md) {
-        const int d = 32 * md + j;
-        uint4 u;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vt + vt_off(d, g0));
-        const uint2 hi = *reinterpret_cast<const uint2*>(vt + vt_off(d, g1));
-        u.x = lo.x;
-        u.y = lo.y;
-        u.z = hi.x;
-        u.w = hi.y;
+        const uint4 u = *reinterpret_cast<const uint4*>(vt + 2048 * md + (v_lane ^ (16 * ks_ ^ 32 * (md & 1))));
         o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u), pf, o[md], 0, 0, 0);
       }
     }
