@@ -19,9 +19,10 @@
 //     keys, so the row max and sum are lane-local plus one exchange with lane ^ 32.
 //   O^T (128 dims x 32 rows) += V^T (128 x 64) . P^T (64 x 32): 4 x 4 MFMAs.
 //     P^T's B operand is the S accumulator itself (rounded to bf16): lane half h
-//     of K-step ks holds keys 16 ks + 4 h + {0..3, 8..11}, and V^T is read from
-//     LDS at exactly those keys. V is stored transposed in LDS ([dim][key]).
-// LDS layouts keep the MFMA operand reads conflict-free (see kKRow, vt_off).
+//     of K-step ks holds keys 16 ks + 4 h + {0..3, 8..11}. V stays row-major in
+//     LDS and the V^T operand at exactly those keys comes from two transposing
+//     LDS reads (ds_read_b64_tr_b16) per MFMA.
+// LDS layouts keep the MFMA operand reads conflict-free (see kKRow, kVRow).
 #include "common.h"
 #include "kernels.h"
 
@@ -33,24 +34,25 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kBM = kTiledRows;  // packed query rows per workgroup
 constexpr int kBN = 64;          // keys per tile
 constexpr int kThreads = 256;
-// LDS per buffer: the K tile row-major with rows padded to 272 bytes, so the
-// 32 rows an A-operand read touches fall in distinct bank groups and every
-// read address is a per-lane base plus a constant; then the V^T tile.
+// LDS per buffer: the K tile and the V tile, both row-major [key][128] with
+// padded rows. K rows are 272 bytes (16 mod 128): the 8 rows one phase of an
+// A-operand read (ds_read_b128) touches fall in 8 distinct 16-byte bank
+// groups. V rows are 288 bytes (32 mod 128): one phase of a transposing read
+// (ds_read_b64_tr_b16) touches 4 rows x 32 bytes, again disjoint. Every read
+// address is a per-lane base plus a compile-time offset.
 constexpr int kKRow = kHead + 8;
+constexpr int kVRow = kHead + 16;
 constexpr int kKTileElems = kBN * kKRow;
-constexpr int kVTileElems = kHead * kBN;
+constexpr int kVTileElems = kBN * kVRow;
 constexpr int kBufElems = kKTileElems + kVTileElems;
 
-// V^T tile, [dim][64 keys], 128-byte rows of eight 16-byte units. The A
-// operand of K-step ks in lane half h needs keys 16 ks + 4 h + {0..3, 8..11}
-// at one dim: those 8 keys form unit 2 ks + h (first 8 bytes keys +0..3,
-// then +8..11), so one ds_read_b128 feeds one MFMA. Units are XOR-swizzled
-// with f(d) = (d ^ (d >> 3)) & 7: eight lanes reading consecutive dims hit
-// eight different units (no conflict); the transposing writes of 16 lanes
-// (dims 8 c + i) pair up two-way.
-__device__ __forceinline__ int vt_off(int d, int granule) {  // granule = 4 keys 4g..4g+3
-  const int unit = ((granule >> 2) << 1) | (granule & 1), half = (granule >> 1) & 1;
-  return d * kBN + 8 * (unit ^ ((d ^ (d >> 3)) & 7)) + 4 * half;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i % 4 of the 8-byte chunks addressed by lanes 4 e + i / 4, e = 0..3.
+__device__ __forceinline__ bf16x4 lds_read_tr(const bf16_t* p) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
@@ -186,24 +188,8 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     bf16_t* vd = kd + kKTileElems;
 #pragma unroll
     for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(kd + (4 * kg + u) * kKRow + 8 * lc) = kr[u];
-    // Transpose 4 keys x 8 dims into 8 dim rows of 4 keys (8 bytes each).
-    const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vr[0]);
-    const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vr[1]);
-    const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&vr[2]);
-    const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&vr[3]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int w = i >> 1;
-      uint2 o;
-      if (i & 1) {
-        o.x = (w0[w] >> 16) | (w1[w] & 0xffff0000u);
-        o.y = (w2[w] >> 16) | (w3[w] & 0xffff0000u);
-      } else {
-        o.x = (w0[w] & 0xffffu) | (w1[w] << 16);
-        o.y = (w2[w] & 0xffffu) | (w3[w] << 16);
-      }
-      *reinterpret_cast<uint2*>(vd + vt_off(8 * lc + i, kg)) = o;
-    }
+    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + (4 * kg + u) * kVRow + 8 * lc) = vr[u];
   };
 
   f32x16 o[4];
@@ -214,12 +200,15 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   float m = -INFINITY, l = 0.f;
   const float sl2 = a.scale_log2;
 
-  // Per-lane LDS bases: the A operand of S reads K row 32 mb + j at dims
-  // 16 kk + 8 h (base + constant); the A operand of P.V reads V^T row
-  // 32 md + j, unit 2 ks + h, whose swizzle splits into a lane part and a
-  // constant: elem = 2048 md + ((64 j + 8 (h ^ fj)) ^ (16 ks ^ 32 (md & 1))).
+  // Per-lane LDS bases. S's A operand reads K row 32 mb + j at dims 16 kk + 8 h.
+  // P.V's A operand (V^T, 32 dims x 16 keys of K-step ks) is two transposing
+  // reads, keys 16 ks + 8 q + 4 h + {0..3} (q = 0, 1): lane i of 16-lane group
+  // g addresses V row 16 ks + 8 q + 4 (g / 2) + i / 4 at dims
+  // 32 md + 16 (g % 2) + 4 (i % 4), and receives dim 32 md + 16 (g % 2) + i
+  // (= 32 md + j) of those 4 keys.
   const int k_lane = j * kKRow + 8 * h;
-  int v_lane = 64 * j + 8 * (h ^ ((j ^ (j >> 3)) & 7));
+  const int vg = lane >> 4, vi = lane & 15;
+  const int v_lane = (4 * (vg >> 1) + (vi >> 2)) * kVRow + 16 * (vg & 1) + 4 * (vi & 3);
 
   const int steps = (t.last + kBN - 1) / kBN;
   if (steps > 0) {
@@ -232,8 +221,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     const int n0 = st * kBN;
     if (st + 1 < steps) load_tile(n0 + kBN);
     const bf16_t* kt = smem + buf * kBufElems;
-    const bf16_t* vt = kt + kKTileElems;
-    asm volatile("" : "+v"(v_lane));  // keep the 32 V^T addresses out of registers across the loop
+    const bf16_t* vt = kt + kKTileElems;  // V tile
 
     // S^T = K . Q^T for keys n0 .. n0 + 63: all 16 K fragments first, then
     // two interleaved MFMA chains.
@@ -302,8 +290,11 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
       const bf16x8 pf = pack8(pv);
 #pragma unroll
       for (int md = 0; md < 4; ++md) {
-        const uint4 u = *reinterpret_cast<const uint4*>(vt + 2048 * md + (v_lane ^ (16 * ks_ ^ 32 * (md & 1))));
-        o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(u), pf, o[md], 0, 0, 0);
+        const bf16_t* vb = vt + v_lane + 16 * ks_ * kVRow + 32 * md;
+        const bf16x4 lo = lds_read_tr(vb);
+        const bf16x4 hi = lds_read_tr(vb + 8 * kVRow);
+        const bf16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[md], 0, 0, 0);
       }
     }
     if (st + 1 < steps) store_tile(buf ^ 1);
