@@ -24,6 +24,11 @@ for p in (os.path.join(ROOT, "pega-omni_amd"), os.path.join(ROOT, "oracle")):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per lm_attend dispatch of the config-3 decode, from rocprofv3
+# FETCH_SIZE + WRITE_SIZE runs scaled by a 1 GiB copy's counts (the summary
+# and commands are in profiles/decode_config3_traffic.md). Re-measure when
+# the decode kernel changes.
+DECODE_CFG3_TRAFFIC_BYTES = 3.267e9
 BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -226,6 +231,56 @@ def dit_bench(stream, steps, warmup, hk=8):
                 frac=round(fl / (launch_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
 
+def measure_peaks(stream):
+    """Measured ceilings on this GPU (libomni_peaks.so): bf16 MFMA TFLOP/s
+    (4 independent 32x32x16 chains per wave), v_exp_f32 and v_fma_f32 lane
+    rates, and a streaming 16-byte nontemporal read of 4 GiB."""
+    import ctypes
+
+    import torch
+
+    L = ctypes.CDLL(os.path.join(ROOT, "pega-omni_amd", "libomni_peaks.so"))
+    P, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    L.omni_peaks_mfma.argtypes = [P, i32, i32, P]
+    L.omni_peaks_valu.argtypes = [P, i32, i32, i32, P]
+    L.omni_peaks_read.argtypes = [P, i64, P, i32, P]
+    L.omni_peaks_lds.argtypes = [P, i32, i32, P]
+    sink = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    sp = ctypes.c_void_p(sink.data_ptr())
+    st = ctypes.c_void_p(stream.cuda_stream)
+
+    def timed(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            t = a.elapsed_time(b) * 1e-3
+            best = t if best is None else min(best, t)
+        return best
+
+    blocks, iters = 2048, 2000
+    t = timed(lambda: L.omni_peaks_mfma(sp, blocks, iters, st))
+    mfma = blocks * 4 * iters * 4 * 32 * 32 * 16 * 2 / t / 1e12
+    vi = 4096
+    t_exp = timed(lambda: L.omni_peaks_valu(sp, blocks, vi, 1, st))
+    t_fma = timed(lambda: L.omni_peaks_valu(sp, blocks, vi, 0, st))
+    lanes = blocks * 256 * vi * 8
+    li = 4096
+    t_lds = timed(lambda: L.omni_peaks_lds(sp, blocks, li, st))
+    lds_bytes = blocks * 256 * li * 8 * 16
+    buf = torch.empty(4 << 30, dtype=torch.uint8, device="cuda")
+    t_rd = timed(lambda: L.omni_peaks_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), sp, 256 * 16, st))
+    del buf
+    return dict(mfma_bf16_tflops=round(mfma, 1), exp_glane_ops=round(lanes / t_exp / 1e9, 1),
+                fma_glane_ops=round(lanes / t_fma / 1e9, 1),
+                lds_read_tbs=round(lds_bytes / t_lds / 1e12, 2), hbm_read_gbs=round((4 << 30) / t_rd / 1e9, 1))
+
+
 def copy_calibration(mb):
     """A plain device copy of `mb` MiB, 5 times: the known-size kernel that
     scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -250,6 +305,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
+    ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
     args = ap.parse_args()
     if args.calib_copy_mib:
         copy_calibration(args.calib_copy_mib)
@@ -264,6 +320,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     stream = torch.cuda.Stream()
     extra = {}
+    if args.peaks or args.only == 0:
+        extra["measured_peaks"] = measure_peaks(stream)
+        log(f"[bench] measured peaks: {extra['measured_peaks']}")
+        if args.peaks:
+            print(json.dumps(extra["measured_peaks"]), flush=True)
+            return
 
     if args.only in (0, 4):
         log("[bench] config 4 prefill")
@@ -339,7 +401,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": DECODE_CFG3_TRAFFIC_BYTES if cfg == 3 else None,
             "kernel": "decode_split<1> + decode_combine (one lm_attend call)",
             "bytes_per_launch": per_launch_bytes,
             "launch_us": round(launch_ms * 1e3, 2),

@@ -1,0 +1,92 @@
+// Peak microbenchmarks for gfx950, used by bench.py to report the measured
+// ceilings next to the published ones: bf16 MFMA throughput, v_exp_f32 and
+// v_fma_f32 issue rates, and streaming HBM read bandwidth. Built into
+// libomni_peaks.so, separate from the attention library.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Four independent 32x32x16 bf16 MFMA chains per wave, `iters` rounds.
+__global__ __launch_bounds__(256) void mfma_loop(float* sink, int iters) {
+  bf16x8 a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (__bf16)(0.001f * (threadIdx.x + i));
+    b[i] = (__bf16)(0.002f * (threadIdx.x - i));
+  }
+  f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int it = 0; it < iters; ++it) {
+    c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c1, 0, 0, 0);
+    c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c2, 0, 0, 0);
+    c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c3, 0, 0, 0);
+  }
+  float s = 0.f;
+  for (int i = 0; i < 16; ++i) s += c0[i] + c1[i] + c2[i] + c3[i];
+  if (s == 1234.5f) sink[threadIdx.x] = s;
+}
+
+// Eight independent v_exp_f32 (or v_fma_f32) chains per lane.
+template <bool EXP>
+__global__ __launch_bounds__(256) void valu_loop(float* sink, int iters) {
+  float x[8];
+  for (int i = 0; i < 8; ++i) x[i] = -0.001f * (threadIdx.x + i);
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = EXP ? __builtin_amdgcn_exp2f(x[i]) - 1.0f : fmaf(x[i], 0.999f, 0.001f);
+  float s = 0.f;
+  for (int i = 0; i < 8; ++i) s += x[i];
+  if (s == 1234.5f) sink[threadIdx.x] = s;
+}
+
+// Streaming read: every thread sums 16-byte words, grid-strided.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void read_stream(const u32x4* p, int64_t n, unsigned* sink) {
+  unsigned acc = 0;
+  for (int64_t i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const u32x4 v = __builtin_nontemporal_load(p + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x12345678u) sink[0] = acc;
+}
+
+// LDS read throughput: each lane reads 16 bytes per ds_read_b128 from a
+// conflict-free pattern, 8 independent reads per round.
+__global__ __launch_bounds__(256) void lds_loop(float* sink, int iters) {
+  __shared__ __align__(16) float buf[16384];
+  for (int i = threadIdx.x; i < 16384; i += 256) buf[i] = (float)i;
+  __syncthreads();
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 acc = {0, 0, 0, 0};
+  int base = (threadIdx.x & 63) * 4 + (threadIdx.x >> 6) * 2048;
+  for (int it = 0; it < iters; ++it) {
+    asm volatile("" : "+v"(base));  // the reads stay inside the loop
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc += *reinterpret_cast<const f4*>(buf + ((base + k * 256) & 0x3FFC));
+  }
+  if (acc.x + acc.y + acc.z + acc.w == 1234.5f) sink[threadIdx.x] = acc.x;
+}
+
+extern "C" {
+int omni_peaks_lds(void* sink, int blocks, int iters, void* stream) {
+  lds_loop<<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+// Each returns 0 or -1; the caller times the launch on `stream`.
+int omni_peaks_mfma(void* sink, int blocks, int iters, void* stream) {
+  mfma_loop<<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+int omni_peaks_valu(void* sink, int blocks, int iters, int exp, void* stream) {
+  if (exp)
+    valu_loop<true><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
+  else
+    valu_loop<false><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+int omni_peaks_read(const void* p, int64_t bytes, void* sink, int blocks, void* stream) {
+  read_stream<<<blocks, 256, 0, (hipStream_t)stream>>>((const u32x4*)p, bytes / 16, (unsigned*)sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+}
