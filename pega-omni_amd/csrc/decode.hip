@@ -18,6 +18,9 @@
 // folded into q, online per tile, the running max shared by the whole wave.
 // V: each lane accumulates p * v for its 8 dims and G heads; rows merge at the
 // end, waves merge in LDS, splits merge in `decode_combine` (log-sum-exp).
+// (Merging in the last-arriving split workgroup needs a device-scope release
+// fence per workgroup, which writes back the L2 on gfx950 and costs far more
+// than the separate combine launch.)
 #include "common.h"
 #include "kernels.h"
 
@@ -50,7 +53,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int t0 = split * a.chunk;
   const int t1 = split == nsplit - 1 ? len : t0 + a.chunk;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: tile starts are scalar
   const int r = lane >> 4, c = lane & 15;
 
   float q[G][8];
@@ -78,12 +82,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   }
 
   for (int tb = t0 + wave * kTileKeys; tb < t1; tb += kDecodeWaves * kTileKeys) {
+    // Key tb + 4 i + r of the tile, clamped to the split (a clamped key has
+    // p = 0 and reads a valid slot). With page >= 4 the four keys 4 i .. 4 i + 3
+    // share a page, so its id is a wave-uniform (scalar) load.
     int64_t off[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      int t = tb + 4 * i + r;
-      t = t < t1 ? t : tb;  // keys past the split read a valid row; their p is 0
-      off[i] = ((((int64_t)pg[t >> shift]) << shift) | (t & pmask)) * per_slot;
+      const int t = min(tb + 4 * i + r, t1 - 1);
+      int64_t pid;
+      if (shift >= 2)
+        pid = pg[min(tb + 4 * i, t1 - 1) >> shift];
+      else
+        pid = pg[t >> shift];
+      off[i] = ((pid << shift) | (t & pmask)) * per_slot;
     }
     uint4 kr[8], vr[8];
 #pragma unroll
@@ -185,7 +196,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   }
 }
 
-// Merge the splits of every (row, q head) that used more than one.
+// Merge the splits of every (row, q head) that used more than one: a
+// workgroup of 128 threads per (q head, row), one thread per dim.
 __global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
   const int h = blockIdx.x, n = blockIdx.y, d = threadIdx.x;
   const int s = a.ragged ? a.seq[n] : n;
