@@ -89,7 +89,7 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.scale_log2 = scale * 1.4426950408889634f;
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d not in {1,2,4}", hq / hk);
-  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(hipGetLastError()));
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
 }
 
@@ -189,7 +189,7 @@ int omni_attn_gather_kv(const void* kv, int hk, const int32_t* indptr, const int
   if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "gather_kv: page=%d is not a power of two", page);
   if (omni::launch_gather_kv(kv, hk, indptr, pages, log2i(page), seq_ids, lens, out_indptr, nseq, out,
                              as_stream(stream)) != 0)
-    return fail(OMNI_ATTN_ELAUNCH, "gather_kv: launch failed");
+    return fail(OMNI_ATTN_ELAUNCH, "gather_kv: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
 }
 
@@ -262,7 +262,7 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
   a.scale_log2 = scale * 1.4426950408889634f;
   const int rc = omni::launch_prefill(a, plan->tiles, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_run: shape not implemented");
-  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "prefill_run: launch failed");
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "prefill_run: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
 }
 
@@ -297,7 +297,8 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
   a.scale_log2 = scale_log2;
   const int rc = omni::launch_dit(a, batch, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: shape not implemented");
-  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed");
+  if (rc != 0)
+    return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
 }
 

@@ -225,10 +225,10 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
     case 4: decode_split<4><<<grid, kDecodeThreads, 0, stream>>>(a); break;
     default: return -2;
   }
-  if (hipGetLastError() != hipSuccess) return -3;
+  if (check_launch() != 0) return -3;
   if (a.splits > 1) {
     decode_combine<<<dim3(a.hq, rows), kHead, 0, stream>>>(a);
-    if (hipGetLastError() != hipSuccess) return -3;
+    if (check_launch() != 0) return -3;
   }
   return 0;
 }
@@ -260,7 +260,7 @@ int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_
   if (nseq == 0) return 0;
   gather_kv_kernel<<<dim3(nseq, 16), 256, 0, stream>>>(static_cast<const uint4*>(kv), hk, indptr, pages, shift,
                                                       seq_ids, lens, out_indptr, static_cast<uint4*>(out));
-  return hipGetLastError() == hipSuccess ? 0 : -3;
+  return check_launch();
 }
 
 }  // namespace omni

@@ -7,6 +7,13 @@ namespace omni {
 
 typedef uint16_t bf16_t;
 
+// The HIP status of this thread's last launch, kept for error messages.
+inline thread_local hipError_t g_launch_status = hipSuccess;
+inline int check_launch() {
+  g_launch_status = hipGetLastError();
+  return g_launch_status == hipSuccess ? 0 : -3;
+}
+
 // Everything a decode launch reads; passed by value as the kernel argument.
 struct DecodeArgs {
   const bf16_t* qkv;

@@ -35,13 +35,14 @@ constexpr int kBM = kTiledRows;  // packed query rows per workgroup
 constexpr int kBN = 64;          // keys per tile
 constexpr int kThreads = 256;
 // LDS per buffer: the K tile and the V tile, both row-major [key][128] with
-// padded rows. K rows are 272 bytes (16 mod 128): the 8 rows one phase of an
-// A-operand read (ds_read_b128) touches fall in 8 distinct 16-byte bank
-// groups. V rows are 288 bytes (32 mod 128): one phase of a transposing read
-// (ds_read_b64_tr_b16) touches 4 rows x 32 bytes, again disjoint. Every read
-// address is a per-lane base plus a compile-time offset.
+// padded rows, for an LDS of 64 banks x 4 bytes (256 bytes per cycle). K rows
+// are 272 bytes (16 mod 256): the 16 lanes of one phase of an A-operand read
+// (ds_read_b128, 16 rows) hit 16 distinct 16-byte bank groups. V rows are 320
+// bytes (64 mod 256): one phase of a transposing read (ds_read_b64_tr_b16,
+// 32 lanes) touches 4 rows x 64 bytes, again disjoint. Every read address is a
+// per-lane base plus a compile-time offset.
 constexpr int kKRow = kHead + 8;
-constexpr int kVRow = kHead + 16;
+constexpr int kVRow = kHead + 32;
 constexpr int kKTileElems = kBN * kKRow;
 constexpr int kVTileElems = kBN * kVRow;
 constexpr int kBufElems = kKTileElems + kVTileElems;
@@ -334,7 +335,7 @@ int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) 
 #undef OMNI_CASE
     default: return -2;
   }
-  return hipGetLastError() == hipSuccess ? 0 : -3;
+  return check_launch();
 }
 
 int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream) {

@@ -83,6 +83,10 @@ def load(path: str = LIB_PATH):
         return _lib
     if not os.path.exists(path):
         raise OmniAttnError(ELAUNCH, f"{path} is missing: build it with pega-omni_amd/build.py")
+    # torch brings its own HIP runtime; load it first so the library binds to
+    # the same one instead of pulling in a second copy from /opt/rocm.
+    import torch  # noqa: F401
+
     L = ctypes.CDLL(path)
     P, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
     dplan = ctypes.POINTER(DecodePlan)
