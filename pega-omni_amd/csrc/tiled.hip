@@ -22,7 +22,7 @@
 //     of K-step ks holds keys 16 ks + 4 h + {0..3, 8..11}. V stays row-major in
 //     LDS and the V^T operand at exactly those keys comes from two transposing
 //     LDS reads (ds_read_b64_tr_b16) per MFMA.
-// LDS layouts keep the MFMA operand reads conflict-free (see kKRow, kVRow).
+// LDS layouts keep the MFMA operand reads conflict-free (see kTileElems).
 #include "common.h"
 #include "kernels.h"
 
@@ -33,19 +33,21 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = kTiledRows;  // packed query rows per workgroup
 constexpr int kBN = 64;          // keys per tile
-constexpr int kThreads = 256;
-// LDS per buffer: the K tile and the V tile, both row-major [key][128] with
-// padded rows, for an LDS of 64 banks x 4 bytes (256 bytes per cycle). K rows
-// are 272 bytes (16 mod 256): the 16 lanes of one phase of an A-operand read
-// (ds_read_b128, 16 rows) hit 16 distinct 16-byte bank groups. V rows are 320
-// bytes (64 mod 256): one phase of a transposing read (ds_read_b64_tr_b16,
-// 32 lanes) touches 4 rows x 64 bytes, again disjoint. Every read address is a
-// per-lane base plus a compile-time offset.
-constexpr int kKRow = kHead + 8;
-constexpr int kVRow = kHead + 32;
-constexpr int kKTileElems = kBN * kKRow;
-constexpr int kVTileElems = kBN * kVRow;
-constexpr int kBufElems = kKTileElems + kVTileElems;
+constexpr int kWaves = kTiledRows / 32;  // one 32-row query block per wave
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWave = kBN / kWaves;  // K/V tile rows each wave loads
+// LDS per buffer: the K tile then the V tile, each [64 keys][128] bf16 in
+// 256-byte rows, filled straight from global memory (global_load_lds_dwordx4:
+// lane l of a wave's load lands at M0 + 16 l, so one load fills 4 rows). The
+// rows are XOR-swizzled for conflict-free operand reads on an LDS of 64 banks
+// x 4 bytes; the swizzle is applied by choosing which global 16-byte chunk
+// each lane loads.
+//   K: 16-byte chunk c of row r sits in slot c ^ (r & 15): the 16 rows of one
+//      phase of an A-operand read (ds_read_b128) hit 16 different slots.
+//   V: 64-byte unit u of row r sits in unit u ^ (r & 3): the 4 rows x 64 bytes
+//      of one phase of a transposing read (ds_read_b64_tr_b16) are disjoint.
+constexpr int kTileElems = kBN * kHead;
+constexpr int kBufElems = 2 * kTileElems;
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     t.vbase = a.v + b * a.kv_bstride + (int64_t)kvh * kHead;
   }
 
-  // Buffer i: K tile at smem + i * kBufElems, V^T tile right after it.
+  // Buffer i: K tile at smem + i * kBufElems, V tile right after it.
   __shared__ __align__(16) bf16_t smem[2 * kBufElems];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -155,42 +157,33 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     __builtin_amdgcn_s_waitcnt(0x0F70);
   }
 
-  // Loader role: keys 4 kg + u (u < 4) of a tile, 16-byte chunk c.
-  const int kg = tid >> 4, lc = tid & 15;
-  uint4 kr[4], vr[4];
-  auto load_tile = [&](int n0) {
-    // Keys n0 + 4 kg + u share one page (page >= 4); past `last` they repeat
-    // the last key, whose scores are masked.
-    const int k0 = min(n0 + 4 * kg, t.last - 1);
-    const int room = t.last - 1 - k0;  // keys k0 + u with u <= room exist
-    const bf16_t* kp;
-    const bf16_t* vp;
-    int64_t step;
-    if constexpr (PAGED) {
-      const int sh = a.page_shift;
-      const int64_t slot = ((int64_t)t.pg[k0 >> sh] << sh) | (k0 & ((1 << sh) - 1));
-      kp = t.kbase + slot * t.per_slot + lc * 8;
-      vp = t.vbase + slot * t.per_slot + lc * 8;
-      step = t.per_slot;
-    } else {
-      kp = t.kbase + (int64_t)k0 * t.kv_stride + lc * 8;
-      vp = t.vbase + (int64_t)k0 * t.kv_stride + lc * 8;
-      step = t.kv_stride;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t off = u <= room ? u * step : 0;
-      kr[u] = ldg16(kp + off);
-      vr[u] = ldg16(vp + off);
-    }
-  };
-  auto store_tile = [&](int buf) {
+  // Loader: wave w fills rows kRowsPerWave w .. of the K and V tiles, four
+  // rows per load; lane l takes row kRowsPerWave w + 4 i + l / 16 and LDS
+  // slot l % 16.
+  // Keys past `last` repeat the last key (their scores are masked).
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  typedef __attribute__((address_space(3))) void lds_void;
+  auto issue_tile = [&](int n0, int buf) {
     bf16_t* kd = smem + buf * kBufElems;
-    bf16_t* vd = kd + kKTileElems;
+    bf16_t* vd = kd + kTileElems;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(kd + (4 * kg + u) * kKRow + 8 * lc) = kr[u];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) *reinterpret_cast<uint4*>(vd + (4 * kg + u) * kVRow + 8 * lc) = vr[u];
+    for (int i = 0; i < kRowsPerWave / 4; ++i) {
+      const int row = kRowsPerWave * wave_u + 4 * i + (lane >> 4);
+      const int key = min(n0 + row, t.last - 1);
+      const int cs = lane & 15;
+      const int kc = cs ^ (row & 15);
+      const int vc = (((cs >> 2) ^ (row & 3)) << 2) | (cs & 3);
+      int64_t off;
+      if constexpr (PAGED) {
+        const int sh = a.page_shift;
+        off = (((int64_t)t.pg[key >> sh] << sh) | (key & ((1 << sh) - 1))) * t.per_slot;
+      } else {
+        off = (int64_t)key * t.kv_stride;
+      }
+      const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;
+      __builtin_amdgcn_global_load_lds(t.kbase + off + 8 * kc, (lds_void*)(kd + lrow), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(t.vbase + off + 8 * vc, (lds_void*)(vd + lrow), 16, 0, 0);
+    }
   };
 
   f32x16 o[4];
@@ -201,28 +194,28 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   float m = -INFINITY, l = 0.f;
   const float sl2 = a.scale_log2;
 
-  // Per-lane LDS bases. S's A operand reads K row 32 mb + j at dims 16 kk + 8 h.
+  // Per-lane LDS bases (elements). S's A operand: K row 32 mb + j, chunk
+  // 2 kk + h, in slot (2 kk + h) ^ (j & 15): elem = (k_lane ^ 16 kk) + 4096 mb.
   // P.V's A operand (V^T, 32 dims x 16 keys of K-step ks) is two transposing
   // reads, keys 16 ks + 8 q + 4 h + {0..3} (q = 0, 1): lane i of 16-lane group
   // g addresses V row 16 ks + 8 q + 4 (g / 2) + i / 4 at dims
-  // 32 md + 16 (g % 2) + 4 (i % 4), and receives dim 32 md + 16 (g % 2) + i
-  // (= 32 md + j) of those 4 keys.
-  const int k_lane = j * kKRow + 8 * h;
+  // 32 md + 16 (g % 2) + 4 (i % 4) (unit md of a row with row % 4 = i / 4),
+  // and receives dim 32 md + j of those 4 keys: elem = (v_lane ^ 32 md) +
+  // (16 ks + 8 q) * 128.
+  const int k_lane = j * kHead + 8 * (h ^ (j & 15));
   const int vg = lane >> 4, vi = lane & 15;
-  const int v_lane = (4 * (vg >> 1) + (vi >> 2)) * kVRow + 16 * (vg & 1) + 4 * (vi & 3);
+  const int v_lane = (4 * (vg >> 1) + (vi >> 2)) * kHead + 32 * (vi >> 2) + 16 * (vg & 1) + 4 * (vi & 3);
 
   const int steps = (t.last + kBN - 1) / kBN;
-  if (steps > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  if (steps > 0) issue_tile(0, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first tile is in LDS
   __syncthreads();
   for (int st = 0; st < steps; ++st) {
     const int buf = st & 1;
     const int n0 = st * kBN;
-    if (st + 1 < steps) load_tile(n0 + kBN);
+    if (st + 1 < steps) issue_tile(n0 + kBN, buf ^ 1);  // lands while this tile computes
     const bf16_t* kt = smem + buf * kBufElems;
-    const bf16_t* vt = kt + kKTileElems;  // V tile
+    const bf16_t* vt = kt + kTileElems;  // V tile
 
     // S^T = K . Q^T for keys n0 .. n0 + 63: all 16 K fragments first, then
     // two interleaved MFMA chains.
@@ -231,7 +224,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk)
-        kf[mb][kk] = *reinterpret_cast<const uint4*>(kt + k_lane + mb * 32 * kKRow + 16 * kk);
+        kf[mb][kk] = *reinterpret_cast<const uint4*>(kt + (k_lane ^ (16 * kk)) + mb * 4096);
     f32x16 sc[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -291,14 +284,14 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
       const bf16x8 pf = pack8(pv);
 #pragma unroll
       for (int md = 0; md < 4; ++md) {
-        const bf16_t* vb = vt + v_lane + 16 * ks_ * kVRow + 32 * md;
+        const bf16_t* vb = vt + (v_lane ^ (32 * md)) + 16 * ks_ * kHead;
         const bf16x4 lo = lds_read_tr(vb);
-        const bf16x4 hi = lds_read_tr(vb + 8 * kVRow);
+        const bf16x4 hi = lds_read_tr(vb + 8 * kHead);
         const bf16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[md], 0, 0, 0);
       }
     }
-    if (st + 1 < steps) store_tile(buf ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
     __syncthreads();
   }
 
