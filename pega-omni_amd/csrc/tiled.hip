@@ -126,8 +126,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     t.vbase = a.v + b * a.kv_bstride + (int64_t)kvh * kHead;
   }
 
-  // Buffer i: K tile at smem + i * kBufElems, V tile right after it.
-  __shared__ __align__(16) bf16_t smem[2 * kBufElems];
+  // Two tile buffers (K tile, then V tile), separate objects so the compiler
+  // can see that loads landing in one never alias reads of the other.
+  __shared__ __align__(16) bf16_t smem0[kBufElems];
+  __shared__ __align__(16) bf16_t smem1[kBufElems];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
@@ -163,8 +165,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   // Keys past `last` repeat the last key (their scores are masked).
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   typedef __attribute__((address_space(3))) void lds_void;
-  auto issue_tile = [&](int n0, int buf) {
-    bf16_t* kd = smem + buf * kBufElems;
+  auto issue_tile = [&](int n0, bf16_t* kd) {
     bf16_t* vd = kd + kTileElems;
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
@@ -207,15 +208,15 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   const int v_lane = (4 * (vg >> 1) + (vi >> 2)) * kHead + 32 * (vi >> 2) + 16 * (vg & 1) + 4 * (vi & 3);
 
   const int steps = (t.last + kBN - 1) / kBN;
-  if (steps > 0) issue_tile(0, 0);
+  if (steps > 0) issue_tile(0, smem0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first tile is in LDS
   __syncthreads();
-  for (int st = 0; st < steps; ++st) {
-    const int buf = st & 1;
+  // One key tile: start loading the next tile into `nxt`, compute from `cur`.
+  auto tile_step = [&](int st, const bf16_t* cur, bf16_t* nxt) {
     const int n0 = st * kBN;
-    if (st + 1 < steps) issue_tile(n0 + kBN, buf ^ 1);  // lands while this tile computes
-    const bf16_t* kt = smem + buf * kBufElems;
-    const bf16_t* vt = kt + kTileElems;  // V tile
+    if (st + 1 < steps) issue_tile(n0 + kBN, nxt);  // lands while this tile computes
+    const bf16_t* kt = cur;
+    const bf16_t* vt = cur + kTileElems;  // V tile
 
     // S^T = K . Q^T for keys n0 .. n0 + 63: all 16 K fragments first, then
     // two interleaved MFMA chains.
@@ -293,6 +294,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
     __syncthreads();
+  };
+  for (int st = 0; st < steps; st += 2) {
+    tile_step(st, smem0, smem1);
+    if (st + 1 < steps) tile_step(st + 1, smem1, smem0);
   }
 
   // Normalise and store: register e of block md is dim 32 md + 8 (e / 4) + 4 h + e % 4.
