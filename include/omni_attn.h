@@ -114,7 +114,8 @@ typedef struct omni_attn_prefill_plan {
 } omni_attn_prefill_plan;
 
 /* Host: validate (seq_h, pos_h) for `rows` ragged rows and write the work list
- * (4 int32 per tile) into work_h (capacity work_cap int32). Returns
+ * into work_h (capacity work_cap int32): 4 int32 per tile (sequence, first
+ * row, rows, keys its last row sees), longest tiles first. Returns
  * OMNI_ATTN_EWORKSPACE with plan->work_bytes set when work_h is too small. */
 int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_t* seq_h, const int32_t* pos_h,
                                 int32_t* work_h, int64_t work_cap, omni_attn_prefill_plan* plan);

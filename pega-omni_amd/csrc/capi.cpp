@@ -5,11 +5,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <array>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <vector>
 
 #include "kernels.h"
 
@@ -221,10 +224,11 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
     while (e < rows && seq_h[e] == seq_h[n] && pos_h[e] == pos_h[e - 1] + 1) ++e;
     for (int f = n; f < e; f += per_tile) {
       if (work_h && (tiles + 1) * 4 <= work_cap) {
+        const int nq = (e - f) < per_tile ? (e - f) : per_tile;
         work_h[tiles * 4 + 0] = seq_h[n];
         work_h[tiles * 4 + 1] = f;
-        work_h[tiles * 4 + 2] = (e - f) < per_tile ? (e - f) : per_tile;
-        work_h[tiles * 4 + 3] = 0;
+        work_h[tiles * 4 + 2] = nq;
+        work_h[tiles * 4 + 3] = pos_h[f + nq - 1] + 1;  // keys the tile's last row sees
       }
       ++tiles;
     }
@@ -235,6 +239,14 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   plan->work_bytes = tiles * 4 * (int64_t)sizeof(int32_t);
   if (!work_h || tiles * 4 > work_cap)
     return fail(OMNI_ATTN_EWORKSPACE, "prefill_plan: work list needs %lld int32", (long long)(tiles * 4));
+  // Longest tiles first: causal tiles differ in length by up to the whole
+  // context, and starting the long ones first keeps short ones for the tail.
+  std::vector<std::array<int32_t, 4>> order(tiles);
+  for (int64_t i = 0; i < tiles; ++i)
+    for (int k = 0; k < 4; ++k) order[i][k] = work_h[i * 4 + k];
+  std::stable_sort(order.begin(), order.end(), [](const auto& x, const auto& y) { return x[3] > y[3]; });
+  for (int64_t i = 0; i < tiles; ++i)
+    for (int k = 0; k < 4; ++k) work_h[i * 4 + k] = order[i][k];
   return ok();
 }
 

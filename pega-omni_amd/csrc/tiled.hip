@@ -88,15 +88,17 @@ struct Tile {
 
 template <int G, bool PAGED>
 __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items, int ntiles) {
-  // XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
+  // DiT, XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
   // contiguous block of work items so the tiles sharing one K/V head (and
   // batch) share that XCD's L2.
+  // Prefill: the work list is longest-first, so items go out in order with
+  // the kv heads of one tile side by side (spread over the XCDs).
   const int per = (items + 7) >> 3;
-  const int idx = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  const int idx = PAGED ? (int)blockIdx.x : (int)((blockIdx.x & 7) * per + (blockIdx.x >> 3));
   if (idx >= items) return;
-  const int tile = idx % ntiles;
-  const int kvh = (idx / ntiles) % a.hk;
-  const int b = idx / (ntiles * a.hk);
+  const int tile = PAGED ? idx / a.hk : idx % ntiles;
+  const int kvh = PAGED ? idx % a.hk : (idx / ntiles) % a.hk;
+  const int b = PAGED ? 0 : idx / (ntiles * a.hk);
   constexpr int kPos = kBM / G;  // positions per tile
 
   Tile t;

@@ -116,8 +116,9 @@ def test_prefill_plan_tiles_cover_every_row_once():
     plan, work = _plan_host(r.rows, 32, 8, r.seq, r.pos)
     per_tile = 128 // 4
     covered = np.zeros(r.rows, int)
-    for s, first, n, _ in work:
-        assert 1 <= n <= per_tile
+    assert np.all(np.diff(work[:, 3]) <= 0), "tiles are longest first"
+    for s, first, n, keys in work:
+        assert 1 <= n <= per_tile and keys == r.pos[first + n - 1] + 1
         assert np.all(r.seq[first:first + n] == s)
         assert np.all(np.diff(r.pos[first:first + n]) == 1)
         covered[first:first + n] += 1
@@ -128,4 +129,4 @@ def test_prefill_plan_breaks_runs_at_position_gaps():
     seq = np.array([0, 0, 0, 1, 1, 0, 0], np.int32)
     pos = np.array([5, 6, 8, 0, 1, 9, 10], np.int32)
     _, work = _plan_host(7, 4, 4, seq, pos)
-    assert [tuple(w[:3]) for w in work] == [(0, 0, 2), (0, 2, 1), (1, 3, 2), (0, 5, 2)]
+    assert [tuple(w) for w in work] == [(0, 5, 2, 11), (0, 2, 1, 9), (0, 0, 2, 7), (1, 3, 2, 2)]
