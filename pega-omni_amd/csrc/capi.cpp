@@ -42,15 +42,16 @@ int log2i(int x) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// Split size for a decode bucket. Each (row, kv head) is split into chunks
-// of `chunk` keys so the whole launch has at least ~8k workgroups at full
-// length (32 per CU on 256 CUs), which evens out skewed lengths; chunks
-// stay between 128 and 1024 keys so a workgroup streams >= 64 KiB of K/V.
+// Split size for a decode bucket: the largest chunk (<= 1024 keys) that
+// still gives the launch >= 2048 split workgroups at full length (8 per CU
+// on 256 CUs), down to 128. Measured on MI355X: a 128-session MHA tick
+// (4096 row x head pairs) runs best unsplit below 1024 keys, the 64-row
+// GQA talker (512 pairs) best at 512.
 int pick_chunk(int rows, int hk, int max_len) {
   int chunk = 1024;
   while (chunk > 128) {
     const long long units = (long long)rows * hk * ((max_len + chunk - 1) / chunk);
-    if (units >= 8192) break;
+    if (units >= 2048) break;
     chunk /= 2;
   }
   return chunk;
