@@ -76,6 +76,15 @@ int omni_lm_attend(const void* qkv, const void* kv, const int32_t* pos, const in
                    const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
                    int context, const omni_attn_decode_plan* plan, void* workspace, void* stream);
 
+/* Replaces `lm_attend` over its real cache format (crates/omni-personaplex/
+ * kernels/lm.cu:196-290): FP8 E4M3 slots of 2 * heads * 128 + 2 * heads * 4
+ * bytes, [K heads x 128 B | V heads x 128 B | K scales f32 x heads | V scales
+ * f32 x heads]; score = q . k * k_scale * scale, V weighted by p * v_scale.
+ * Same arguments as omni_lm_attend; the plan is made with hq = hk = heads. */
+int omni_lm_attend_fp8(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                       const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
+                       int context, const omni_attn_decode_plan* plan, void* workspace, void* stream);
+
 /* Same kernels with the FlashInfer-style length encoding the engines can also
  * produce: sequence s holds (indptr[s+1] - indptr[s] - 1) * page +
  * last_page_len[s] tokens, and row n (sequence ragged ? seq[n] : n) sees all

@@ -18,6 +18,9 @@
  *   oracle_dense_attend   crates/omni-hidream-o1/kernels/hidream.cu:209-347
  *                         (hidream_attend: base-2 online softmax over 64-key tiles,
  *                         P rounded to bf16 before P.V, l from unrounded P)
+ *   oracle_lm_attend_fp8  crates/omni-personaplex/kernels/lm.cu:196-290 (lm_attend over
+ *                         FP8 E4M3 slots with per-(slot, head) f32 scales), with
+ *                         oracle_e4m3_to_f32 the OCP E4M3 decode
  *   oracle_fill_normal_bf16 / oracle_splitmix64  the synthetic-input rule
  *
  * Arithmetic follows the reference kernels: f32 accumulation, per-tile online
@@ -330,5 +333,122 @@ int oracle_dense_attend(const bf16_t* q, const bf16_t* k, const bf16_t* v, bf16_
   if (hk <= 0 || hq % hk != 0) return -1;
   dense_args a = {q, k, v, out, q_len, kv_len, q_stride, hq, hk, causal, scale_log2};
   run_items(dense_item, &a, (int64_t)q_len * hq, nthreads);
+  return 0;
+}
+
+/* ------------------------------------------- FP8 (E4M3) ring attention */
+
+/* OCP FP8 E4M3 ("e4m3fn": bias 7, no infinities, S.1111.111 is NaN, max 448,
+ * subnormals m * 2^-9) to f32, exactly. */
+float oracle_e4m3_to_f32(uint8_t b) {
+  const int s = b >> 7, e = (b >> 3) & 15, m = b & 7;
+  float v;
+  if (e == 15 && m == 7)
+    v = NAN;
+  else if (e == 0)
+    v = ldexpf((float)m, -9);
+  else
+    v = ldexpf((float)(8 + m), e - 10);
+  return s ? -v : v;
+}
+
+typedef struct {
+  const bf16_t* qkv;
+  const uint8_t* kv;
+  const int32_t* pos;
+  const int32_t* seq;
+  int ragged;
+  const int32_t* indptr;
+  const int32_t* pages;
+  int page;
+  bf16_t* out;
+  int heads;
+  float scale;
+  int context;
+} fp8_args;
+
+/* One (row n, head h) item of lm_attend (lm.cu:196-290): slot =
+ * [K heads x 128 B | V heads x 128 B | K scales (f32 x heads) | V scales];
+ * s = dot(q, k) * (k_scale * scale); p * v_scale weights the fp8 V row.
+ * 4 warps x 32-key tiles with natural-exp online softmax, then the warp merge
+ * with empty warps contributing 0, as attend_row_fp8. */
+static void fp8_item(void* vctx, int64_t item) {
+  const fp8_args* a = (const fp8_args*)vctx;
+  const int H = a->heads;
+  const int n = (int)(item / H), h = (int)(item % H);
+  const int s = a->ragged ? a->seq[n] : n;
+  int len = a->pos[n] + 1;
+  if (len > a->context) len = a->context;
+  const int64_t slot_bytes = 2LL * H * HEAD + 2LL * H * 4;
+  const bf16_t* q = a->qkv + (int64_t)n * 3 * H * HEAD + (int64_t)h * HEAD;
+  float qs[HEAD];
+  for (int d = 0; d < HEAD; ++d) qs[d] = bf2f(q[d]);
+  float M[WARPS], L[WARPS], O[WARPS][HEAD];
+  for (int w = 0; w < WARPS; ++w) {
+    float m = -INFINITY, l = 0.f;
+    float* acc = O[w];
+    for (int d = 0; d < HEAD; ++d) acc[d] = 0.f;
+    for (int base = w * LANES; base < len; base += WARPS * LANES) {
+      float sv[LANES], pv[LANES];
+      int64_t slot[LANES];
+      float tmax = -INFINITY;
+      for (int lane = 0; lane < LANES; ++lane) {
+        const int t = base + lane;
+        const int valid = t < len;
+        slot[lane] = oracle_slot(a->indptr, a->pages, s, valid ? t : base, a->page);
+        const uint8_t* sp = a->kv + slot[lane] * slot_bytes;
+        const uint8_t* k = sp + (int64_t)h * HEAD;
+        float ks, vs;
+        memcpy(&ks, sp + 2LL * H * HEAD + (int64_t)h * 4, 4);
+        memcpy(&vs, sp + 2LL * H * HEAD + (int64_t)(H + h) * 4, 4);
+        float dot = 0.f;
+        for (int c = 0; c < HEAD; c += 8) {
+          float part = qs[c] * oracle_e4m3_to_f32(k[c]);
+          for (int e = 1; e < 8; ++e) part += qs[c + e] * oracle_e4m3_to_f32(k[c + e]);
+          dot += part;
+        }
+        sv[lane] = valid ? dot * (ks * a->scale) : -INFINITY;
+        pv[lane] = vs;
+        if (sv[lane] > tmax) tmax = sv[lane];
+      }
+      const float m2 = fmaxf(m, tmax);
+      const float corr = expf(m - m2);
+      float p[LANES];
+      for (int lane = 0; lane < LANES; ++lane) p[lane] = expf(sv[lane] - m2);
+      l = l * corr + bfly_sum(p);
+      for (int d = 0; d < HEAD; ++d) acc[d] *= corr;
+      m = m2;
+      const int count = len - base < LANES ? len - base : LANES;
+      for (int j = 0; j < count; ++j) {
+        const float pvj = p[j] * pv[j];
+        const uint8_t* v = a->kv + slot[j] * slot_bytes + (int64_t)(H + h) * HEAD;
+        for (int d = 0; d < HEAD; ++d) acc[d] += pvj * oracle_e4m3_to_f32(v[d]);
+      }
+    }
+    M[w] = m;
+    L[w] = l;
+  }
+  float top = -INFINITY;
+  for (int w = 0; w < WARPS; ++w) top = fmaxf(top, M[w]);
+  for (int d = 0; d < HEAD; ++d) {
+    float num = 0.f, den = 0.f;
+    for (int w = 0; w < WARPS; ++w) {
+      const float e = M[w] == -INFINITY ? 0.f : expf(M[w] - top);
+      num += O[w][d] * e;
+      den += L[w] * e;
+    }
+    a->out[((int64_t)n * H + h) * HEAD + d] = f2bf(num / den);
+  }
+}
+
+/* lm_attend over FP8 E4M3 slots (crates/omni-personaplex/kernels/lm.cu:
+ * 196-290): MHA, qkv rows [3 heads][128] bf16, slot bytes 2*heads*128 +
+ * 2*heads*4, rows see min(pos + 1, context) ring slots. */
+int oracle_lm_attend_fp8(const bf16_t* qkv, const uint8_t* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                         const int32_t* indptr, const int32_t* pages, int page, bf16_t* out, int rows, int heads,
+                         float scale, int context, int nthreads) {
+  if (heads <= 0 || page <= 0) return -1;
+  fp8_args a = {qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, scale, context > 0 ? context : 0x7fffffff};
+  run_items(fp8_item, &a, (int64_t)rows * heads, nthreads);
   return 0;
 }

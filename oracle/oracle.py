@@ -12,6 +12,7 @@ the pega-omni tree):
   (``qwen3_attend``) and, with ``context``, ``crates/omni-personaplex/kernels/
   lm.cu:273-290`` (``lm_attend``) over bf16 slots (``attend.cuh:41-106``).
 * :func:`dense_attend`  — ``crates/omni-hidream-o1/kernels/hidream.cu:209-347``.
+* :func:`lm_attend_fp8` — ``crates/omni-personaplex/kernels/lm.cu:196-290`` (FP8 E4M3 slots).
 * :func:`gather_kv` / :func:`slot` — ``qwen3.cu:210-214`` (``PagedSlots``).
 """
 from __future__ import annotations
@@ -51,6 +52,10 @@ def lib():
         L.oracle_slot.restype = i64
         L.oracle_fill_normal_bf16.argtypes = [P, i64, u64]
         L.oracle_fill_normal_bf16.restype = None
+        L.oracle_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.oracle_e4m3_to_f32.restype = ctypes.c_float
+        L.oracle_lm_attend_fp8.argtypes = [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, i32, i32]
+        L.oracle_lm_attend_fp8.restype = i32
         _lib = L
     return _lib
 
@@ -105,6 +110,23 @@ def dense_attend(q, k, v, q_len, kv_len, q_stride, hq, hk, causal, scale_log2, n
                                    float(scale_log2), int(nthreads))
     if rc != 0:
         raise ValueError("oracle_dense_attend: unsupported shape")
+    return out
+
+
+def e4m3_to_f32(b: int) -> float:
+    return float(lib().oracle_e4m3_to_f32(b))
+
+
+def lm_attend_fp8(qkv, kv, pos, seq, ragged, indptr, pages, page, heads, scale, context, nthreads=1):
+    """lm_attend over FP8 E4M3 slots (lm.cu:196-290). kv is uint8
+    [slots][2*heads*128 + 2*heads*4]. Returns out uint16 [rows][heads*128]."""
+    rows = int(pos.shape[0])
+    out = np.zeros((rows, heads * 128), dtype=np.uint16)
+    seq = np.ascontiguousarray(seq if seq is not None else np.zeros(rows, np.int32), dtype=np.int32)
+    rc = lib().oracle_lm_attend_fp8(_p(qkv), _p(kv), _p(pos), _p(seq), int(ragged), _p(indptr), _p(pages), page,
+                                    _p(out), rows, heads, float(scale), int(context), int(nthreads))
+    if rc != 0:
+        raise ValueError("oracle_lm_attend_fp8: unsupported shape")
     return out
 
 

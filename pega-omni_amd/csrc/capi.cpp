@@ -59,7 +59,8 @@ int pick_chunk(int rows, int hk, int max_len) {
 
 int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
                   const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
-                  int context, int len_mode, const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+                  int context, int len_mode, const omni_attn_decode_plan* plan, void* workspace, void* stream,
+                  int fp8 = 0) {
   if (!plan) return fail(OMNI_ATTN_EINVAL, "decode: null plan");
   if (plan->hq != hq || plan->hk != hk || plan->page != page)
     return fail(OMNI_ATTN_EINVAL, "decode: plan was made for hq=%d hk=%d page=%d, called with hq=%d hk=%d page=%d",
@@ -91,6 +92,8 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.chunk = plan->chunk;
   a.splits = plan->splits;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.fp8 = fp8;
+  a.slot_bytes = 2LL * hk * OMNI_ATTN_HEAD_DIM + 2LL * hk * 4;
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d not in {1,2,4}", hq / hk);
   if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(omni::g_launch_status));
@@ -143,6 +146,14 @@ int omni_lm_attend(const void* qkv, const void* kv, const int32_t* pos, const in
   if (context <= 0) return fail(OMNI_ATTN_EINVAL, "lm_attend: context=%d", context);
   return decode_common(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, heads, scale, context, 0, plan,
                        workspace, stream);
+}
+
+int omni_lm_attend_fp8(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                       const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
+                       int context, const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  if (context <= 0) return fail(OMNI_ATTN_EINVAL, "lm_attend_fp8: context=%d", context);
+  return decode_common(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, heads, scale, context, 0, plan,
+                       workspace, stream, 1);
 }
 
 int omni_attn_decode_run_lastlen(const void* qkv, const void* kv, const int32_t* last_page_len, const int32_t* seq,

@@ -50,6 +50,7 @@ constexpr int kQuadSwap1 = 0xB1;      // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kQuadSwap2 = 0x4E;      // quad_perm [2,3,0,1]: lane ^ 2
 constexpr int kRowHalfMirror = 0x141; // lane i <- 7 - i within each 8
 constexpr int kRowMirror = 0x140;     // lane i <- 15 - i within each 16
+constexpr int kRowRor8 = 0x128;       // lane i <- (i + 8) % 16 within each 16: lane ^ 8
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
 __device__ __forceinline__ float row16_sum(float v) {

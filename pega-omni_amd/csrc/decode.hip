@@ -43,6 +43,34 @@ __device__ __forceinline__ int decode_nsplit(const DecodeArgs& a, int len) {
   return len <= a.chunk ? 1 : min(a.splits, (len + a.chunk - 1) / a.chunk);
 }
 
+// Merge the four waves' (m, l, o) of one (split, kv head, row) workgroup and
+// write the row's output (one split) or the split's normalised partial.
+template <int G>
+__device__ __forceinline__ void merge_waves(const DecodeArgs& a, int n, int kh, int split, int nsplit, int len,
+                                            const float (*sm_m)[G], const float (*sm_l)[G],
+                                            const float (*sm_o)[G][kHead]) {
+  for (int i = threadIdx.x; i < G * kHead; i += kDecodeThreads) {
+    const int g = i / kHead, d = i % kHead;
+    float top = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) top = fmaxf(top, sm_m[w][g]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; ++w) {
+      const float e = sm_m[w][g] == -INFINITY ? 0.f : fast_exp2(sm_m[w][g] - top);
+      num = fmaf(sm_o[w][g][d], e, num);
+      den = fmaf(sm_l[w][g], e, den);
+    }
+    const int64_t h = (int64_t)n * a.hq + kh * G + g;
+    if (nsplit == 1) {
+      a.out[h * kHead + d] = (bf16_t)f2bf(len > 0 ? num / den : 0.f);
+    } else {
+      a.ws_o[(h * a.splits + split) * kHead + d] = num / den;
+      if (d == 0) a.ws_lse[h * a.splits + split] = top + __log2f(den);
+    }
+  }
+}
+
 template <int G>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
@@ -174,26 +202,176 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < G * kHead; i += kDecodeThreads) {
-    const int g = i / kHead, d = i % kHead;
-    float top = -INFINITY;
+  merge_waves<G>(a, n, kh, split, nsplit, len, sm_m, sm_l, sm_o);
+}
+
+// ------------------------------------------------------------------ FP8 slots
+//
+// lm_attend's real cache (crates/omni-personaplex/kernels/lm.cu:196-290): a
+// slot is [K heads x 128 B | V heads x 128 B | K scales f32 x hk | V scales
+// f32 x hk] with FP8 E4M3 values; score = dot(q, k) * k_scale * scale and the
+// V row is weighted by p * v_scale. Same split-K structure as the bf16 kernel,
+// with 128-byte head rows: a row of 8 lanes owns one key (16 E4M3 values =
+// 16 dims per lane, one 16-byte load), so a load instruction moves 8 keys and
+// a 32-key tile takes 4 loads of K and 4 of V. E4M3 widens to f32 on the
+// hardware converter (v_cvt_pk_f32_fp8, OCP E4M3 on gfx950).
+
+typedef float f32x2_fp8_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void widen16_fp8(const uint4& u, float* v) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) top = fmaxf(top, sm_m[w][g]);
-    float num = 0.f, den = 0.f;
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_fp8_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+    const f32x2_fp8_t hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+    v[4 * i + 0] = lo.x;
+    v[4 * i + 1] = lo.y;
+    v[4 * i + 2] = hi.x;
+    v[4 * i + 3] = hi.y;
+  }
+}
+
+// Sum over the 8 lanes of a half DPP row; every lane of the 8 gets the sum.
+__device__ __forceinline__ float row8_sum(float v) {
+  v += dpp<kQuadSwap1>(v);
+  v += dpp<kQuadSwap2>(v);
+  v += dpp<kRowHalfMirror>(v);
+  return v;
+}
+
+template <int G>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a) {
+  const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
+  const int s = a.ragged ? a.seq[n] : n;
+  const int len = decode_len(a, n, s);
+  const int nsplit = decode_nsplit(a, len);
+  if (split >= nsplit) return;
+  const int t0 = split * a.chunk;
+  const int t1 = split == nsplit - 1 ? len : t0 + a.chunk;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane >> 3, c = lane & 7;  // key row r of 8, dims 16 c .. 16 c + 15
+
+  float q[G][16];
+  const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * G * kHead + c * 16;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) {
-      const float e = sm_m[w][g] == -INFINITY ? 0.f : fast_exp2(sm_m[w][g] - top);
-      num = fmaf(sm_o[w][g][d], e, num);
-      den = fmaf(sm_l[w][g], e, den);
+  for (int g = 0; g < G; ++g) {
+    widen8(ldg16(qp + g * kHead), q[g]);
+    widen8(ldg16(qp + g * kHead + 8), q[g] + 8);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[g][e] *= a.scale_log2;
+  }
+
+  const int32_t* pg = a.pages + a.indptr[s];
+  const uint8_t* kvb = reinterpret_cast<const uint8_t*>(a.kv);
+  const int64_t sb = a.slot_bytes;
+  const int64_t koff = (int64_t)kh * kHead + c * 16, voff = (int64_t)(a.hk + kh) * kHead + c * 16;
+  const int64_t ksoff = 2LL * a.hk * kHead + kh * 4, vsoff = 2LL * a.hk * kHead + (a.hk + kh) * 4;
+  const int shift = a.page_shift, pmask = (1 << shift) - 1;
+
+  float m[G], l[G], acc[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[g][e] = 0.f;
+  }
+
+  for (int tb = t0 + wave * kTileKeys; tb < t1; tb += kDecodeWaves * kTileKeys) {
+    // Key tb + 8 i + r, clamped to the split (a clamped key has p = 0).
+    const uint8_t* sp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = min(tb + 8 * i + r, t1 - 1);
+      const int64_t pid = shift >= 3 ? pg[min(tb + 8 * i, t1 - 1) >> shift] : pg[t >> shift];
+      sp[i] = kvb + ((pid << shift) | (t & pmask)) * sb;
     }
-    const int64_t h = (int64_t)n * a.hq + kh * G + g;
-    if (nsplit == 1) {
-      a.out[h * kHead + d] = (bf16_t)f2bf(len > 0 ? num / den : 0.f);
-    } else {
-      a.ws_o[(h * a.splits + split) * kHead + d] = num / den;
-      if (d == 0) a.ws_lse[h * a.splits + split] = top + __log2f(den);
+    uint4 kr[4], vr[4];
+    float ks[4], vs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kr[i] = ldg16(sp[i] + koff);
+      vr[i] = ldg16(sp[i] + voff);
+      ks[i] = *reinterpret_cast<const float*>(sp[i] + ksoff);
+      vs[i] = *reinterpret_cast<const float*>(sp[i] + vsoff);
+    }
+    float sc[G][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float kf[16];
+      widen16_fp8(kr[i], kf);
+      const bool valid = tb + 8 * i + r < t1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) d = fmaf(q[g][e], kf[e], d);
+        d = row8_sum(d) * ks[i];
+        sc[g][i] = valid ? d : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = fmaxf(fmaxf(sc[g][0], sc[g][1]), fmaxf(sc[g][2], sc[g][3]));
+      mx = fmaxf(mx, dpp<kRowRor8>(mx));  // the other 8-lane row of the DPP row
+      mx = fmaxf(mx, xor_lane(mx, 16));
+      mx = fmaxf(mx, xor_lane(mx, 32));
+      const float mn = fmaxf(m[g], mx);
+      const float corr = fast_exp2(m[g] - mn);
+      m[g] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[g][i] = fast_exp2(sc[g][i] - mn);
+        ps += sc[g][i];
+      }
+      l[g] = fmaf(l[g], corr, ps);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[g][e] *= corr;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float vf[16];
+      widen16_fp8(vr[i], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pv = sc[g][i] * vs[i];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[g][e] = fmaf(pv, vf[e], acc[g][e]);
+      }
     }
   }
+
+  // The 8 key rows of the wave hold disjoint keys under one shared max.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] += dpp<kRowRor8>(l[g]);
+    l[g] += xor_lane(l[g], 16);
+    l[g] += xor_lane(l[g], 32);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      acc[g][e] += dpp<kRowRor8>(acc[g][e]);
+      acc[g][e] += xor_lane(acc[g][e], 16);
+      acc[g][e] += xor_lane(acc[g][e], 32);
+    }
+  }
+  __shared__ float sm_m[kDecodeWaves][G], sm_l[kDecodeWaves][G];
+  __shared__ float sm_o[kDecodeWaves][G][kHead];
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sm_o[wave][g][c * 16 + e] = acc[g][e];
+      if (c == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+  merge_waves<G>(a, n, kh, split, nsplit, len, sm_m, sm_l, sm_o);
 }
 
 // Merge the splits of every (row, q head) that used more than one: a
@@ -219,10 +397,13 @@ __global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   const dim3 grid(a.splits, a.hk, rows);
-  switch (a.hq / a.hk) {
+  switch ((a.hq / a.hk) * (a.fp8 ? -1 : 1)) {
     case 1: decode_split<1><<<grid, kDecodeThreads, 0, stream>>>(a); break;
     case 2: decode_split<2><<<grid, kDecodeThreads, 0, stream>>>(a); break;
     case 4: decode_split<4><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+    case -1: decode_split_fp8<1><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+    case -2: decode_split_fp8<2><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+    case -4: decode_split_fp8<4><<<grid, kDecodeThreads, 0, stream>>>(a); break;
     default: return -2;
   }
   if (check_launch() != 0) return -3;

@@ -29,6 +29,7 @@ EXPORTS = (
     "omni_attn_decode_plan_init",
     "omni_qwen3_attend",
     "omni_lm_attend",
+    "omni_lm_attend_fp8",
     "omni_attn_decode_run_lastlen",
     "omni_attn_check_table",
     "omni_attn_gather_kv",
@@ -95,6 +96,7 @@ def load(path: str = LIB_PATH):
         "omni_attn_decode_plan_init": [i32, i32, i32, i32, i32, i32, dplan],
         "omni_qwen3_attend": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
         "omni_lm_attend": [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, dplan, P, P],
+        "omni_lm_attend_fp8": [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, dplan, P, P],
         "omni_attn_decode_run_lastlen": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
         "omni_attn_check_table": [P, i32, P, i32, P, P, i32, i32, i32, i32],
         "omni_attn_gather_kv": [P, i32, P, P, i32, P, P, P, i32, P, P],
@@ -200,6 +202,23 @@ def lm_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, scale,
     _check(load().omni_lm_attend(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr), _ptr(pages),
                                  page, _ptr(out), heads, float(scale), context, ctypes.byref(plan), _ptr(workspace),
                                  _stream(stream)))
+    return out
+
+
+def lm_attend_fp8(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, scale, context, plan, workspace=None,
+                  stream=None):
+    """``lm_attend`` over FP8 E4M3 slots (crates/omni-personaplex/kernels/lm.cu:196-290).
+    kv is a uint8 device tensor of slots of 2*heads*128 + 2*heads*4 bytes."""
+    import torch
+
+    _bf16_dev(qkv, "qkv"), _bf16_dev(out, "out")
+    if kv.dtype != torch.uint8 or not kv.is_cuda or not kv.is_contiguous():
+        raise OmniAttnError(EINVAL, "kv must be a contiguous uint8 device tensor of FP8 slots")
+    for t, n in ((pos, "pos"), (seq, "seq"), (indptr, "indptr"), (pages, "pages")):
+        _i32_dev(t, n)
+    _check(load().omni_lm_attend_fp8(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr),
+                                     _ptr(pages), page, _ptr(out), heads, float(scale), context, ctypes.byref(plan),
+                                     _ptr(workspace), _stream(stream)))
     return out
 
 

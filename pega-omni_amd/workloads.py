@@ -200,3 +200,50 @@ def config_case(cfg: int, seed: int | None = None, values="host", layer=0):
                                    c["cached_hi"], seed=seed, values=values, slack_pages=16, name=f"config{cfg}")
     return dense_case(c["hq"], c["hk"], c["q_len"], c["kv_len"], 0, batch=c["batch"], seed=seed, values=values,
                       name=f"config{cfg}")
+
+
+# ------------------------------------------------------------- FP8 ring slots
+def fp8_slot_bytes(heads: int) -> int:
+    """PersonaPlex slot: [K heads x 128 B | V heads x 128 B | K scales f32 x heads
+    | V scales f32 x heads] (crates/omni-personaplex/kernels/lm.cu:123-128)."""
+    return 2 * heads * HEAD + 2 * heads * 4
+
+
+def quantize_fp8_slots(kv: np.ndarray, heads: int) -> np.ndarray:
+    """f32 K/V [slots][2 heads][128] -> FP8 E4M3 slots [slots][slot_bytes], each
+    (slot, head) row scaled by max(amax / 448, 1e-12) as lm_rope does
+    (lm.cu:148-176), rounded to nearest even by torch's float8_e4m3fn cast."""
+    import torch
+
+    slots = kv.shape[0]
+    x = torch.from_numpy(np.ascontiguousarray(kv, dtype=np.float32)).view(slots, 2 * heads, HEAD)
+    amax = x.abs().amax(dim=-1, keepdim=True)
+    sc = torch.clamp(amax * (1.0 / 448.0), min=1e-12)
+    q8 = (x / sc).to(torch.float8_e4m3fn).view(torch.uint8).reshape(slots, 2 * heads * HEAD)
+    out = np.empty((slots, fp8_slot_bytes(heads)), dtype=np.uint8)
+    out[:, : 2 * heads * HEAD] = q8.numpy()
+    out[:, 2 * heads * HEAD:] = sc.reshape(slots, 2 * heads).numpy().astype(np.float32).view(np.uint8).reshape(
+        slots, 8 * heads)
+    return out
+
+
+def fp8_ring_case(rows, heads, len_lo, len_hi, context, page=16, seed=0, slack_pages=0):
+    """PersonaPlex decode rows over FP8 slots: a bf16-layout PagedCase whose
+    `kv` is replaced by FP8 slot bytes (extra['kv_f32'] keeps the source)."""
+    c = paged_decode_case(rows, heads, heads, len_lo, len_hi, page=page, seed=seed, context=context,
+                          slack_pages=slack_pages)
+    rng = np.random.default_rng(seed + 1)
+    kv = rng.standard_normal((c.num_pages * page, 2 * heads, HEAD), dtype=np.float32)
+    c.kv = quantize_fp8_slots(kv, heads)
+    c.extra["fp8"] = True
+    return c
+
+
+def fp8_kv_bytes(case) -> int:
+    """Algorithmic bytes of one FP8 decode launch: per attended key and head
+    128 B of K, 128 B of V and the two f32 scales; q, out, page ids, indptr, pos."""
+    ln = case.lens()
+    kvb = int(ln.sum()) * case.hk * (2 * HEAD + 8)
+    qo = case.rows * case.hq * HEAD * 2 * 2
+    idx = int(np.ceil(ln / case.page).sum()) * 4 + 4 * len(case.indptr) + 4 * case.rows
+    return kvb + qo + idx

@@ -191,3 +191,51 @@ def test_dense_kv_len_masks_tail(oracle):
     v2[37:] = 0x7FC0
     b = oracle.dense_attend(case.q[0], k2, v2, 10, 37, case.q_stride, 4, 2, 0, case.scale_log2)
     assert np.array_equal(a, b)
+
+
+# ------------------------------------------------------- FP8 (E4M3) ring attention
+def test_e4m3_decode_matches_torch(oracle):
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = np.array([oracle.e4m3_to_f32(int(b)) for b in codes], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan) and np.array_equal(got[~nan], want[~nan])
+
+
+def _dequant(c, heads):
+    raw = c.kv[:, : 2 * heads * 128].copy()
+    vals = torch.from_numpy(raw).view(torch.float8_e4m3fn).float().numpy().reshape(len(raw), 2 * heads, 128)
+    sc = c.kv[:, 2 * heads * 128:].copy().view(np.float32).reshape(len(raw), 2 * heads, 1)
+    return vals.astype(np.float64) * sc
+
+
+@pytest.mark.parametrize("heads,ctx", [(2, 0), (4, 150)])
+def test_fp8_ring_matches_f64_sdpa(oracle, heads, ctx):
+    import workloads as W2
+
+    c = W2.fp8_ring_case(6, heads, 1, 300, ctx, seed=heads + ctx)
+    got = oracle.lm_attend_fp8(c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, 16, heads, c.scale, ctx or 0)
+    deq = _dequant(c, heads)
+    from refs import slots_of
+    want = np.zeros((c.rows, heads, 128))
+    for n in range(c.rows):
+        sl = slots_of(c, n, int(c.lens()[n]))
+        k = torch.from_numpy(deq[sl, :heads].transpose(1, 0, 2).copy())
+        v = torch.from_numpy(deq[sl, heads:].transpose(1, 0, 2).copy())
+        q = torch.from_numpy(bits_to_f64(c.qkv[n, : heads * 128]).reshape(heads, 1, 128))
+        want[n] = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=c.scale)[:, 0].numpy()
+    ok, worst = within_ulp(got, want)
+    assert ok, worst
+
+
+def test_fp8_single_key_is_scaled_v_row(oracle):
+    import workloads as W2
+
+    c = W2.fp8_ring_case(3, 2, 1, 1, 0, seed=31)
+    got = oracle.lm_attend_fp8(c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, 16, 2, c.scale, 0)
+    for n in range(c.rows):
+        slot = int(c.pages[c.indptr[n]]) * 16
+        v8 = torch.from_numpy(c.kv[slot, 2 * 128: 4 * 128].copy()).view(torch.float8_e4m3fn).float().numpy()
+        vs = c.kv[slot, 4 * 128:].copy().view(np.float32)[2:4]
+        want = W.f32_to_bf16_bits((v8.reshape(2, 128) * vs[:, None]).astype(np.float32)).reshape(-1)
+        assert np.array_equal(got[n], want)
