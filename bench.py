@@ -36,12 +36,30 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def fp8_pool(slots, heads, gen):
+    """A device pool of FP8 E4M3 slots holding N(0,1) K/V, quantized per
+    (slot, head) with scale max(amax / 448, 1e-12) as lm_rope writes them."""
+    import torch
+
+    import workloads as W
+
+    kv8 = torch.empty(slots, W.fp8_slot_bytes(heads), dtype=torch.uint8, device="cuda")
+    body = 2 * heads * 128
+    for s0 in range(0, slots, 16384):
+        s1 = min(slots, s0 + 16384)
+        x = torch.randn(s1 - s0, 2 * heads, 128, device="cuda", generator=gen)
+        sc = torch.clamp(x.abs().amax(-1, keepdim=True) / 448.0, min=1e-12)
+        kv8[s0:s1, :body] = (x / sc).to(torch.float8_e4m3fn).view(torch.uint8).reshape(s1 - s0, body)
+        kv8[s0:s1, body:] = sc.reshape(s1 - s0, 2 * heads).contiguous().view(torch.uint8)
+    return kv8
+
+
 class DecodeBench:
     """Device-resident decode workload: `pools` distinct K/V pools (each far
     larger than the 256 MB last-level cache) cycled over the layers, each
     layer with its own random page table."""
 
-    def __init__(self, cfg, pools, seed=0, chunk=0):
+    def __init__(self, cfg, pools, seed=0, chunk=0, fp8=False):
         import numpy as np
         import torch
 
@@ -52,6 +70,8 @@ class DecodeBench:
         c = W.CONFIGS[cfg]
         self.layers = c["layers"]
         self.lm = cfg == 3
+        self.fp8 = fp8
+        assert not fp8 or self.lm, "FP8 slots are PersonaPlex's (config 3) cache format"
         self.cases, self.dev = [], []
         gen = torch.Generator(device="cuda").manual_seed(seed + cfg)
         for layer in range(self.layers):
@@ -61,8 +81,11 @@ class DecodeBench:
         pool_pages = max(cs.num_pages for cs in self.cases)
         for i in range(min(pools, self.layers)):
             case = self.cases[i]
-            kv = torch.empty(pool_pages * case.page, 2 * case.hk * 128, dtype=torch.bfloat16, device="cuda")
-            kv.normal_(generator=gen)
+            if fp8:
+                kv = fp8_pool(pool_pages * case.page, case.hk, gen)
+            else:
+                kv = torch.empty(pool_pages * case.page, 2 * case.hk * 128, dtype=torch.bfloat16, device="cuda")
+                kv.normal_(generator=gen)
             self.pools.append(kv)
         for layer, case in enumerate(self.cases):
             kv = self.pools[layer % len(self.pools)]
@@ -76,12 +99,15 @@ class DecodeBench:
         c0 = self.cases[0]
         self.plan = oa.decode_plan(c0.rows, c0.hq, c0.hk, c0.page, c["len_hi"] if not self.lm else c["context"], chunk)
         self.ws = oa.workspace_for(self.plan)
-        self.bytes_per_layer = [cs.kv_bytes() for cs in self.cases]
+        self.bytes_per_layer = [W.fp8_kv_bytes(cs) if fp8 else cs.kv_bytes() for cs in self.cases]
         self.oa = oa
 
     def layer(self, i, stream):
         d, c = self.dev[i], self.cases[i]
-        if self.lm:
+        if self.fp8:
+            self.oa.lm_attend_fp8(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page,
+                                  d["out"], c.hq, c.scale, c.context, self.plan, self.ws, stream)
+        elif self.lm:
             self.oa.lm_attend(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page, d["out"],
                               c.hq, c.scale, c.context, self.plan, self.ws, stream)
         else:
@@ -303,7 +329,7 @@ def main():
     ap.add_argument("--pools", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5)")
+    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
     args = ap.parse_args()
@@ -349,7 +375,19 @@ def main():
         log(f"[bench] {extra['config2']}")
         del b2
         torch.cuda.empty_cache()
-    if args.only in (4, 5, 2):
+    if args.only in (0, 6):
+        log("[bench] config 3 decode over FP8 E4M3 slots")
+        b8 = DecodeBench(3, args.pools, chunk=args.chunk, fp8=True)
+        ms8, l8 = time_steps(lambda s, e: b8.step(s, e), args.steps, args.warmup, stream, per_launch=b8.layers)
+        tb = sum(b8.bytes_per_layer)
+        extra["config3_fp8"] = dict(workload="config3 over PersonaPlex FP8 E4M3 slots (8448 B per slot)",
+                                    ms_per_step=round(ms8, 4), gbs=round(tb / (ms8 * 1e-3) / 1e9, 1),
+                                    launch_us=round(l8 * 1e3, 2), chunk=b8.plan.chunk,
+                                    frac=round(tb / b8.layers / (l8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        log(f"[bench] {extra['config3_fp8']}")
+        del b8
+        torch.cuda.empty_cache()
+    if args.only in (4, 5, 2, 6):
         print(json.dumps({"extra": extra}), flush=True)
         return
 
@@ -402,7 +440,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": DECODE_CFG3_TRAFFIC_BYTES if cfg == 3 else None,
-            "kernel": "decode_split<1> + decode_combine (one lm_attend call)",
+            "kernel": "decode_split<1, true> + decode_combine (one lm_attend call)",
             "bytes_per_launch": per_launch_bytes,
             "launch_us": round(launch_ms * 1e3, 2),
         },

@@ -71,6 +71,9 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   if (plan->splits > 1 && (!workspace || plan->workspace_bytes <= 0))
     return fail(OMNI_ATTN_EWORKSPACE, "decode: plan needs %lld workspace bytes", (long long)plan->workspace_bytes);
   if (!std::isfinite(scale)) return fail(OMNI_ATTN_EINVAL, "decode: non-finite scale");
+  const int gh = plan->group_heads;
+  if (fp8 && gh != 0 && (gh < 0 || (gh & (gh - 1)) != 0 || gh > 8 || hk % gh != 0))
+    return fail(OMNI_ATTN_EINVAL, "decode: plan group_heads=%d is not 1, 2, 4 or 8 dividing heads=%d", gh, hk);
   omni::DecodeArgs a{};
   a.qkv = static_cast<const omni::bf16_t*>(qkv);
   a.q_stride = (int64_t)(hq + 2 * hk) * OMNI_ATTN_HEAD_DIM;
@@ -94,6 +97,7 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.scale_log2 = scale * 1.4426950408889634f;
   a.fp8 = fp8;
   a.slot_bytes = 2LL * hk * OMNI_ATTN_HEAD_DIM + 2LL * hk * 4;
+  a.group_heads = plan->group_heads;
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d not in {1,2,4}", hq / hk);
   if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(omni::g_launch_status));

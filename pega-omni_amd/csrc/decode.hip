@@ -39,8 +39,17 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int n, int s) {
   return min(len, a.context);
 }
 
-__device__ __forceinline__ int decode_nsplit(const DecodeArgs& a, int len) {
-  return len <= a.chunk ? 1 : min(a.splits, (len + a.chunk - 1) / a.chunk);
+// Keys per split of a row of `len` keys: ceil(len / chunk) splits (at most
+// the plan's), of equal length rounded up to 32 keys, so no split is a short
+// remainder. A multiple of 32 keeps every key group a kernel loads inside one
+// page when page >= the group.
+__device__ __forceinline__ int decode_split_len(const DecodeArgs& a, int len) {
+  const int ns = len <= a.chunk ? 1 : min(a.splits, (len + a.chunk - 1) / a.chunk);
+  return ((len + ns - 1) / ns + 31) & ~31;
+}
+
+__device__ __forceinline__ int decode_nsplit(int len, int split_len) {
+  return len <= 0 ? 1 : (len + split_len - 1) / split_len;
 }
 
 // Merge the four waves' (m, l, o) of one (split, kv head, row) workgroup and
@@ -71,15 +80,18 @@ __device__ __forceinline__ void merge_waves(const DecodeArgs& a, int n, int kh, 
   }
 }
 
-template <int G>
+// UP: every group of 4 key rows (page >= 4) lies in one page, so its page id is
+// one wave-uniform scalar load; otherwise each lane loads its own.
+template <int G, bool UP>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
   const int s = a.ragged ? a.seq[n] : n;
   const int len = decode_len(a, n, s);
-  const int nsplit = decode_nsplit(a, len);
+  const int split_len = decode_split_len(a, len);
+  const int nsplit = decode_nsplit(len, split_len);
   if (split >= nsplit) return;
-  const int t0 = split * a.chunk;
-  const int t1 = split == nsplit - 1 ? len : t0 + a.chunk;
+  const int t0 = split * split_len;
+  const int t1 = min(len, t0 + split_len);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: tile starts are scalar
@@ -109,26 +121,38 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
 
-  for (int tb = t0 + wave * kTileKeys; tb < t1; tb += kDecodeWaves * kTileKeys) {
-    // Key tb + 4 i + r of the tile, clamped to the split (a clamped key has
-    // p = 0 and reads a valid slot). With page >= 4 the four keys 4 i .. 4 i + 3
-    // share a page, so its id is a wave-uniform (scalar) load.
+  // Key tb + 4 i + r of a tile, clamped to the split (a clamped key has p = 0
+  // and reads a valid slot). Page ids are loaded one tile ahead, so the K/V
+  // loads of a tile never wait on its page-table reads.
+  auto page_of = [&](int tb, int i) -> int {
+    if constexpr (UP)
+      return pg[__builtin_amdgcn_readfirstlane(min(tb + 4 * i, t1 - 1) >> shift)];
+    else
+      return pg[min(tb + 4 * i + r, t1 - 1) >> shift];
+  };
+  constexpr int kStride = kDecodeWaves * kTileKeys;
+  int pid[8];
+  const int tb0 = t0 + wave * kTileKeys;
+  if (tb0 < t1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pid[i] = page_of(tb0, i);
+  }
+  for (int tb = tb0; tb < t1; tb += kStride) {
     int64_t off[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int t = min(tb + 4 * i + r, t1 - 1);
-      int64_t pid;
-      if (shift >= 2)
-        pid = pg[min(tb + 4 * i, t1 - 1) >> shift];
-      else
-        pid = pg[t >> shift];
-      off[i] = ((pid << shift) | (t & pmask)) * per_slot;
+      off[i] = (((int64_t)pid[i] << shift) | (t & pmask)) * per_slot;
     }
     uint4 kr[8], vr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) kr[i] = ldg16(kb + off[i]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) vr[i] = ldg16(vb + off[i]);
+    if (tb + kStride < t1) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + kStride, i);
+    }
 
     float sc[G][8];
 #pragma unroll
@@ -208,13 +232,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
 // ------------------------------------------------------------------ FP8 slots
 //
 // lm_attend's real cache (crates/omni-personaplex/kernels/lm.cu:196-290): a
-// slot is [K heads x 128 B | V heads x 128 B | K scales f32 x hk | V scales
-// f32 x hk] with FP8 E4M3 values; score = dot(q, k) * k_scale * scale and the
-// V row is weighted by p * v_scale. Same split-K structure as the bf16 kernel,
-// with 128-byte head rows: a row of 8 lanes owns one key (16 E4M3 values =
-// 16 dims per lane, one 16-byte load), so a load instruction moves 8 keys and
-// a 32-key tile takes 4 loads of K and 4 of V. E4M3 widens to f32 on the
-// hardware converter (v_cvt_pk_f32_fp8, OCP E4M3 on gfx950).
+// slot is [K heads x 128 B | V heads x 128 B | K scales f32 x heads | V scales
+// f32 x heads] with FP8 E4M3 values; score = dot(q, k) * k_scale * scale and
+// the V row is weighted by p * v_scale. MHA (one q head per K/V head), as
+// lm_attend is.
+//
+// A workgroup takes H adjacent heads of one (row, split). Lane l works on head
+// kh0 + (l % 8H) / 8, dims 16 (l % 8) .. + 15 (one 16-byte load of 16 E4M3
+// values), key row l / 8H: a load instruction covers R = 8 / H keys, each an
+// H * 128-byte contiguous run of K (and of V), and one scale word load serves
+// H heads from one sector. E4M3 widens to f32 on the hardware converter
+// (v_cvt_pk_f32_fp8, OCP E4M3 on gfx950).
 
 typedef float f32x2_fp8_t __attribute__((ext_vector_type(2)));
 
@@ -231,7 +259,7 @@ __device__ __forceinline__ void widen16_fp8(const uint4& u, float* v) {
   }
 }
 
-// Sum over the 8 lanes of a half DPP row; every lane of the 8 gets the sum.
+// Sum over the 8 lanes of an aligned lane octet.
 __device__ __forceinline__ float row8_sum(float v) {
   v += dpp<kQuadSwap1>(v);
   v += dpp<kQuadSwap2>(v);
@@ -239,28 +267,41 @@ __device__ __forceinline__ float row8_sum(float v) {
   return v;
 }
 
-template <int G>
+// Combine the R = 8 / H key rows of a wave (lanes 8H apart), per lane.
+template <int H, bool MAX>
+__device__ __forceinline__ float across_key_rows(float v) {
+  if constexpr (H == 1) v = MAX ? fmaxf(v, dpp<kRowRor8>(v)) : v + dpp<kRowRor8>(v);
+  if constexpr (H <= 2) v = MAX ? fmaxf(v, xor_lane(v, 16)) : v + xor_lane(v, 16);
+  if constexpr (H <= 4) v = MAX ? fmaxf(v, xor_lane(v, 32)) : v + xor_lane(v, 32);
+  return v;
+}
+
+// NI load instructions (NI * R keys) per wave and iteration. UP: the R keys of
+// one instruction share a page (page >= R), so its id is a scalar load.
+template <int H, int NI, bool UP>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a) {
-  const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
+  constexpr int R = 8 / H;
+  const int split = blockIdx.x, kg = blockIdx.y, n = blockIdx.z;
   const int s = a.ragged ? a.seq[n] : n;
   const int len = decode_len(a, n, s);
-  const int nsplit = decode_nsplit(a, len);
+  const int split_len = decode_split_len(a, len);
+  const int nsplit = decode_nsplit(len, split_len);
   if (split >= nsplit) return;
-  const int t0 = split * a.chunk;
-  const int t1 = split == nsplit - 1 ? len : t0 + a.chunk;
+  const int t0 = split * split_len;
+  const int t1 = min(len, t0 + split_len);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane >> 3, c = lane & 7;  // key row r of 8, dims 16 c .. 16 c + 15
+  const int r = lane / (8 * H), hl = (lane % (8 * H)) >> 3, c = lane & 7;
+  const int kh = kg * H + hl;
 
-  float q[G][16];
-  const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * G * kHead + c * 16;
+  float q[16];
+  {
+    const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * kHead + c * 16;
+    widen8(ldg16(qp), q);
+    widen8(ldg16(qp + 8), q + 8);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    widen8(ldg16(qp + g * kHead), q[g]);
-    widen8(ldg16(qp + g * kHead + 8), q[g] + 8);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) q[g][e] *= a.scale_log2;
+    for (int e = 0; e < 16; ++e) q[e] *= a.scale_log2;
   }
 
   const int32_t* pg = a.pages + a.indptr[s];
@@ -270,108 +311,118 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a)
   const int64_t ksoff = 2LL * a.hk * kHead + kh * 4, vsoff = 2LL * a.hk * kHead + (a.hk + kh) * 4;
   const int shift = a.page_shift, pmask = (1 << shift) - 1;
 
-  float m[G], l[G], acc[G][16];
+  float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[g][e] = 0.f;
-  }
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
 
-  for (int tb = t0 + wave * kTileKeys; tb < t1; tb += kDecodeWaves * kTileKeys) {
-    // Key tb + 8 i + r, clamped to the split (a clamped key has p = 0).
-    const uint8_t* sp[4];
+  constexpr int kKeys = R * NI;  // keys per wave per iteration
+  // Key tb + R i + r, clamped to the split (a clamped key has p = 0 and reads
+  // a valid slot). Two register tiles: the loads of the next tile are in
+  // flight while this one is computed, and page ids are read a tile earlier
+  // still. The tile after the split's last is loaded too, unconditionally
+  // (all its keys clamp to slot t1 - 1, already cached), so every wait is a
+  // plain in-order count.
+  auto page_of = [&](int tb, int i) -> int {
+    if constexpr (UP)
+      return pg[__builtin_amdgcn_readfirstlane(min(tb + R * i, t1 - 1) >> shift)];
+    else
+      return pg[min(tb + R * i + r, t1 - 1) >> shift];
+  };
+  struct Tile {
+    uint4 kr[NI], vr[NI];
+    float ks[NI], vs[NI];
+  };
+  auto load_tile = [&](Tile& x, int tb, const int* pid) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = min(tb + 8 * i + r, t1 - 1);
-      const int64_t pid = shift >= 3 ? pg[min(tb + 8 * i, t1 - 1) >> shift] : pg[t >> shift];
-      sp[i] = kvb + ((pid << shift) | (t & pmask)) * sb;
+    for (int i = 0; i < NI; ++i) {
+      const int t = min(tb + R * i + r, t1 - 1);
+      const uint8_t* sp = kvb + (((int64_t)pid[i] << shift) | (t & pmask)) * sb;
+      x.kr[i] = ldg16(sp + koff);
+      x.vr[i] = ldg16(sp + voff);
+      x.ks[i] = *reinterpret_cast<const float*>(sp + ksoff);
+      x.vs[i] = *reinterpret_cast<const float*>(sp + vsoff);
     }
-    uint4 kr[4], vr[4];
-    float ks[4], vs[4];
+  };
+  auto compute_tile = [&](const Tile& x, int tb) {
+    float sc[NI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kr[i] = ldg16(sp[i] + koff);
-      vr[i] = ldg16(sp[i] + voff);
-      ks[i] = *reinterpret_cast<const float*>(sp[i] + ksoff);
-      vs[i] = *reinterpret_cast<const float*>(sp[i] + vsoff);
-    }
-    float sc[G][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
       float kf[16];
-      widen16_fp8(kr[i], kf);
-      const bool valid = tb + 8 * i + r < t1;
+      widen16_fp8(x.kr[i], kf);
+      float d = 0.f;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) d = fmaf(q[g][e], kf[e], d);
-        d = row8_sum(d) * ks[i];
-        sc[g][i] = valid ? d : -INFINITY;
-      }
+      for (int e = 0; e < 16; ++e) d = fmaf(q[e], kf[e], d);
+      d = row8_sum(d) * x.ks[i];
+      sc[i] = tb + R * i + r < t1 ? d : -INFINITY;
     }
+    float mx = sc[0];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mx = fmaxf(fmaxf(sc[g][0], sc[g][1]), fmaxf(sc[g][2], sc[g][3]));
-      mx = fmaxf(mx, dpp<kRowRor8>(mx));  // the other 8-lane row of the DPP row
-      mx = fmaxf(mx, xor_lane(mx, 16));
-      mx = fmaxf(mx, xor_lane(mx, 32));
-      const float mn = fmaxf(m[g], mx);
-      const float corr = fast_exp2(m[g] - mn);
-      m[g] = mn;
-      float ps = 0.f;
+    for (int i = 1; i < NI; ++i) mx = fmaxf(mx, sc[i]);
+    mx = across_key_rows<H, true>(mx);
+    const float mn = fmaxf(m, mx);
+    const float corr = fast_exp2(m - mn);
+    m = mn;
+    float ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[g][i] = fast_exp2(sc[g][i] - mn);
-        ps += sc[g][i];
-      }
-      l[g] = fmaf(l[g], corr, ps);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[g][e] *= corr;
+    for (int i = 0; i < NI; ++i) {
+      sc[i] = fast_exp2(sc[i] - mn);
+      ps += sc[i];
     }
+    l = fmaf(l, corr, ps);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int e = 0; e < 16; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
       float vf[16];
-      widen16_fp8(vr[i], vf);
+      widen16_fp8(x.vr[i], vf);
+      const float pv = sc[i] * x.vs[i];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pv = sc[g][i] * vs[i];
+      for (int e = 0; e < 16; ++e) acc[e] = fmaf(pv, vf[e], acc[e]);
+    }
+  };
+  constexpr int kStride = kDecodeWaves * kKeys;
+  const int tb0 = t0 + wave * kKeys;
+  if (tb0 < t1) {
+    int pid[NI];
+    Tile ta, tb_;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[g][e] = fmaf(pv, vf[e], acc[g][e]);
-      }
+    for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0, i);
+    load_tile(ta, tb0, pid);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0 + kStride, i);
+    for (int tb = tb0;; tb += 2 * kStride) {
+      load_tile(tb_, tb + kStride, pid);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + 2 * kStride, i);
+      __builtin_amdgcn_sched_barrier(0);  // keep the next tile's loads ahead of this tile's math
+      compute_tile(ta, tb);
+      if (tb + kStride >= t1) break;
+      load_tile(ta, tb + 2 * kStride, pid);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + 3 * kStride, i);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_tile(tb_, tb + kStride);
+      if (tb + 2 * kStride >= t1) break;
     }
   }
 
-  // The 8 key rows of the wave hold disjoint keys under one shared max.
+  // The key rows of the wave hold disjoint keys under one shared max.
+  l = across_key_rows<H, false>(l);
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    l[g] += dpp<kRowRor8>(l[g]);
-    l[g] += xor_lane(l[g], 16);
-    l[g] += xor_lane(l[g], 32);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      acc[g][e] += dpp<kRowRor8>(acc[g][e]);
-      acc[g][e] += xor_lane(acc[g][e], 16);
-      acc[g][e] += xor_lane(acc[g][e], 32);
-    }
-  }
-  __shared__ float sm_m[kDecodeWaves][G], sm_l[kDecodeWaves][G];
-  __shared__ float sm_o[kDecodeWaves][G][kHead];
+  for (int e = 0; e < 16; ++e) acc[e] = across_key_rows<H, false>(acc[e]);
+  __shared__ float sm_m[kDecodeWaves][H], sm_l[kDecodeWaves][H];
+  __shared__ float sm_o[kDecodeWaves][H][kHead];
   if (r == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sm_o[wave][g][c * 16 + e] = acc[g][e];
-      if (c == 0) {
-        sm_m[wave][g] = m[g];
-        sm_l[wave][g] = l[g];
-      }
+    for (int e = 0; e < 16; ++e) sm_o[wave][hl][c * 16 + e] = acc[e];
+    if (c == 0) {
+      sm_m[wave][hl] = m;
+      sm_l[wave][hl] = l;
     }
   }
   __syncthreads();
-  merge_waves<G>(a, n, kh, split, nsplit, len, sm_m, sm_l, sm_o);
+  // Heads kg H .. kg H + H - 1 are q heads kh G + g of merge_waves with G = H.
+  merge_waves<H>(a, n, kg, split, nsplit, len, sm_m, sm_l, sm_o);
 }
 
 // Merge the splits of every (row, q head) that used more than one: a
@@ -380,7 +431,7 @@ __global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
   const int h = blockIdx.x, n = blockIdx.y, d = threadIdx.x;
   const int s = a.ragged ? a.seq[n] : n;
   const int len = decode_len(a, n, s);
-  const int nsplit = decode_nsplit(a, len);
+  const int nsplit = decode_nsplit(len, decode_split_len(a, len));
   if (nsplit <= 1) return;
   const int64_t hh = (int64_t)n * a.hq + h;
   const float* lse = a.ws_lse + hh * a.splits;
@@ -395,17 +446,54 @@ __global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
   a.out[hh * kHead + d] = (bf16_t)f2bf(num / den);
 }
 
-int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
-  const dim3 grid(a.splits, a.hk, rows);
-  switch ((a.hq / a.hk) * (a.fp8 ? -1 : 1)) {
-    case 1: decode_split<1><<<grid, kDecodeThreads, 0, stream>>>(a); break;
-    case 2: decode_split<2><<<grid, kDecodeThreads, 0, stream>>>(a); break;
-    case 4: decode_split<4><<<grid, kDecodeThreads, 0, stream>>>(a); break;
-    case -1: decode_split_fp8<1><<<grid, kDecodeThreads, 0, stream>>>(a); break;
-    case -2: decode_split_fp8<2><<<grid, kDecodeThreads, 0, stream>>>(a); break;
-    case -4: decode_split_fp8<4><<<grid, kDecodeThreads, 0, stream>>>(a); break;
+// Heads per workgroup: the most that still leaves about 4 workgroups per CU.
+static int fp8_heads_per_group(const DecodeArgs& a, int rows) {
+  if (a.group_heads) return a.group_heads;
+  for (int h = 8; h > 1; h >>= 1)
+    if (a.hk % h == 0 && (int64_t)rows * (a.hk / h) * a.splits >= 2048) return h;
+  return 1;
+}
+
+template <int H>
+static void launch_fp8_h(const DecodeArgs& a, int rows, hipStream_t stream) {
+  const dim3 grid(a.splits, a.hk / H, rows);
+  constexpr int R = 8 / H;
+  if (a.page_shift >= __builtin_ctz(R))
+    decode_split_fp8<H, 4, true><<<grid, kDecodeThreads, 0, stream>>>(a);
+  else
+    decode_split_fp8<H, 4, false><<<grid, kDecodeThreads, 0, stream>>>(a);
+}
+
+static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) {
+  if (a.hq != a.hk) return -2;
+  switch (fp8_heads_per_group(a, rows)) {
+    case 8: launch_fp8_h<8>(a, rows, stream); break;
+    case 4: launch_fp8_h<4>(a, rows, stream); break;
+    case 2: launch_fp8_h<2>(a, rows, stream); break;
+    case 1: launch_fp8_h<1>(a, rows, stream); break;
     default: return -2;
   }
+  if (check_launch() != 0) return -3;
+  if (a.splits > 1) {
+    decode_combine<<<dim3(a.hq, rows), kHead, 0, stream>>>(a);
+    if (check_launch() != 0) return -3;
+  }
+  return 0;
+}
+
+int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
+  const dim3 grid(a.splits, a.hk, rows);
+  if (a.fp8) return launch_decode_fp8(a, rows, stream);
+  const bool up = a.page_shift >= 2;
+#define OMNI_DECODE(K, ...) \
+  (up ? K<__VA_ARGS__, true><<<grid, kDecodeThreads, 0, stream>>>(a) : K<__VA_ARGS__, false><<<grid, kDecodeThreads, 0, stream>>>(a))
+  switch (a.hq / a.hk) {
+    case 1: OMNI_DECODE(decode_split, 1); break;
+    case 2: OMNI_DECODE(decode_split, 2); break;
+    case 4: OMNI_DECODE(decode_split, 4); break;
+    default: return -2;
+  }
+#undef OMNI_DECODE
   if (check_launch() != 0) return -3;
   if (a.splits > 1) {
     decode_combine<<<dim3(a.hq, rows), kHead, 0, stream>>>(a);

@@ -35,6 +35,7 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale times log2(e)
   int fp8;           // 1: kv slots are FP8 E4M3 with f32 scales (lm_attend's cache)
   int64_t slot_bytes;  // bytes per FP8 slot: 2 hk 128 + 2 hk 4
+  int group_heads;     // FP8: heads per workgroup (0 = pick from the shape)
 };
 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream);

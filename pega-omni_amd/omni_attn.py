@@ -57,7 +57,7 @@ class DecodePlan(ctypes.Structure):
         ("max_len", ctypes.c_int32),
         ("chunk", ctypes.c_int32),
         ("splits", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("group_heads", ctypes.c_int32),  # FP8 kernel: heads per workgroup, 0 = auto
         ("workspace_bytes", ctypes.c_int64),
     ]
 

@@ -69,6 +69,17 @@ def test_run_without_workspace_fails_before_launch():
     assert rc == oa.EINVAL
 
 
+@pytest.mark.parametrize("gh", [3, 16, -2, 6])
+def test_fp8_group_heads_validated_before_launch(gh):
+    p = oa.decode_plan(4, 8, 8, 16, 1000, chunk=128)
+    p.group_heads = gh
+    fake = ctypes.c_void_p(16)
+    rc = oa.load().omni_lm_attend_fp8(fake, fake, fake, None, 0, fake, fake, 16, fake, 8, 0.1, 1000, ctypes.byref(p),
+                                      fake, None)
+    assert rc == oa.EINVAL
+    assert "group_heads" in oa.load().omni_attn_last_error().decode()
+
+
 def test_check_table_accepts_generated_cases():
     c = W.paged_decode_case(9, 8, 4, 1, 500, seed=1)
     oa.check_table(c.indptr, c.pages, c.num_pages, c.pos, None, False, 16)

@@ -11,9 +11,10 @@ from gpu_util import assert_close, dev_bits, dev_i32, host_bits
 pytestmark = pytest.mark.gpu
 
 
-def run_fp8(c, heads, chunk=0, max_len=None):
+def run_fp8(c, heads, chunk=0, max_len=None, group_heads=0):
     max_len = max_len or int(c.lens().max())
     plan = oa.decode_plan(c.rows, heads, heads, c.page, max_len, chunk)
+    plan.group_heads = group_heads
     out = torch.zeros(c.rows, heads * 128, dtype=torch.bfloat16, device="cuda")
     kv = torch.from_numpy(np.ascontiguousarray(c.kv)).cuda()
     oa.lm_attend_fp8(dev_bits(c.qkv), kv, dev_i32(c.pos), dev_i32(c.seq), c.ragged, dev_i32(c.indptr),
@@ -34,6 +35,15 @@ def oracle_fp8(oracle, c, heads):
 def test_fp8_parity(oracle, heads, lo, hi, ctx, chunk):
     c = W.fp8_ring_case(7, heads, lo, hi, ctx, seed=heads * 7 + lo, slack_pages=3)
     assert_close(run_fp8(c, heads, chunk), oracle_fp8(oracle, c, heads), what=f"fp8 h{heads} ctx{ctx}")
+
+
+@pytest.mark.parametrize("gh", [1, 2, 4, 8])
+@pytest.mark.parametrize("page", [1, 4, 16])
+def test_fp8_heads_per_workgroup(oracle, gh, page):
+    """Every heads-per-workgroup layout (1/2/4/8 heads, 8/4/2/1 keys per load),
+    over pages smaller and larger than a load's key group."""
+    c = W.fp8_ring_case(5, 8, 1, 700, 500, page=page, seed=gh * 31 + page, slack_pages=2)
+    assert_close(run_fp8(c, 8, 128, group_heads=gh), oracle_fp8(oracle, c, 8), what=f"fp8 gh{gh} page{page}")
 
 
 def test_fp8_single_key_exact(oracle):
