@@ -70,18 +70,20 @@ int omni_qwen3_attend(const void* qkv, const void* kv, const int32_t* pos, const
                       const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
                       const omni_attn_decode_plan* plan, void* workspace, void* stream);
 
-/* Replaces `lm_attend` (crates/omni-personaplex/kernels/lm.cu:275-290) over
- * bf16 slots: MHA with `heads` query and K/V heads, qkv rows [3 heads][128],
- * each row sees min(pos[n] + 1, context) ring slots through its page table. */
+/* `lm_attend`'s semantics (crates/omni-personaplex/kernels/lm.cu:273-290) over
+ * bf16 slots (the layout of attend.cuh's bf16 attend_row, attend.cuh:41-106):
+ * MHA with `heads` query and K/V heads, qkv rows [3 heads][128], each row sees
+ * min(pos[n] + 1, context) ring slots through its page table. */
 int omni_lm_attend(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
                    const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
                    int context, const omni_attn_decode_plan* plan, void* workspace, void* stream);
 
-/* Replaces `lm_attend` over its real cache format (crates/omni-personaplex/
- * kernels/lm.cu:196-290): FP8 E4M3 slots of 2 * heads * 128 + 2 * heads * 4
+/* Replaces `lm_attend` itself (crates/omni-personaplex/kernels/lm.cu:273-290,
+ * attend_row_fp8 at lm.cu:196-271), over its cache format: FP8 E4M3 slots of 2 * heads * 128 + 2 * heads * 4
  * bytes, [K heads x 128 B | V heads x 128 B | K scales f32 x heads | V scales
  * f32 x heads]; score = q . k * k_scale * scale, V weighted by p * v_scale.
- * Same arguments as omni_lm_attend; the plan is made with hq = hk = heads. */
+ * Same arguments as omni_lm_attend; the plan is made with hq = hk = heads
+ * (its group_heads may fix the heads per workgroup). */
 int omni_lm_attend_fp8(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
                        const int32_t* indptr, const int32_t* pages, int page, void* out, int heads, float scale,
                        int context, const omni_attn_decode_plan* plan, void* workspace, void* stream);
