@@ -155,6 +155,44 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
                                 const int32_t* kv_len_at, int q_stride, int causal, float scale_log2, int hq, int hk,
                                 int batch, int64_t q_bstride, int64_t kv_bstride, int64_t out_bstride, void* stream);
 
+/* ------------------------------------------ rotary embedding + K/V scatter */
+
+/* The step before attention: rotary embedding of each new row's q (in place)
+ * and k, and K and V written to the row's cache slot. One workgroup per (row,
+ * 16 heads); `rows` is the launch size the reference gives as its grid. */
+
+/* Replaces `qwen3_rope` (crates/omni-qwen3/kernels/qwen3.cu:64-103): per-head
+ * RMSNorm of q and k (f32, x * rsqrt(mean(x^2) + eps) rounded to bf16, times
+ * the bf16 weight), half-split rotary (pair i = elements i, i + 64, angle
+ * pos * theta^(-2i/128)), q in place in qkv rows [(hq + 2 hk)][128], K and V
+ * to slot `slots[n]` of the bf16 paged cache [slot][2 hk][128]. */
+int omni_qwen3_rope(void* qkv, const void* q_norm, const void* k_norm, const int32_t* pos, const int32_t* slots,
+                    void* kv, int rows, int hq, int hk, float eps, float theta, void* stream);
+
+/* Replaces `qwen3_rope_dense` (qwen3.cu:105-111): `per` consecutive rows per
+ * sequence at positions base, base + 1, ..., slot seq * span + pos of a dense
+ * workspace (base + per <= span). */
+int omni_qwen3_rope_dense(void* qkv, const void* q_norm, const void* k_norm, void* kv, int rows, int per, int base,
+                          int span, int hq, int hk, float eps, float theta, void* stream);
+
+/* Replaces `lm_rope` (crates/omni-personaplex/kernels/lm.cu:125-182):
+ * interleaved rotary (pair i = elements 2i, 2i + 1, angle pos * exp(i * coef))
+ * of q in place and of k, then K and V quantized to FP8 E4M3 (round to
+ * nearest even) with per-(slot, head) scale max(amax / 448, 1e-12) into the
+ * slot layout omni_lm_attend_fp8 reads. kv must be 8-byte aligned. */
+int omni_lm_rope(void* qkv, const int32_t* pos, const int32_t* slots, void* kv, int rows, int heads, float coef,
+                 void* stream);
+
+/* Replaces `hidream_qk_rope` (crates/omni-hidream-o1/kernels/hidream.cu:55-106):
+ * RMSNorm as qwen3_rope, then Qwen3-VL's interleaved M-RoPE: row n has
+ * positions (t, h, w) at positions[3n..3n+2]; pair i turns by the h position
+ * when i % 3 == 1 and by w when i % 3 == 2, while i < 3 * mrope_hw, else by t.
+ * q in place (rows of `ld` elements), K and V to slot `slots[n]` of the
+ * separate caches [slots][hk][128]. */
+int omni_hidream_qk_rope(void* qkv, int ld, const void* q_norm, const void* k_norm, const int32_t* positions,
+                         const int32_t* slots, void* k_cache, void* v_cache, int rows, int hq, int hk, int mrope_hw,
+                         float eps, float theta, void* stream);
+
 /* ------------------------------------------------------------- library */
 
 /* Library version (major * 10000 + minor * 100 + patch). */

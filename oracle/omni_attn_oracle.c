@@ -21,6 +21,12 @@
  *   oracle_lm_attend_fp8  crates/omni-personaplex/kernels/lm.cu:196-290 (lm_attend over
  *                         FP8 E4M3 slots with per-(slot, head) f32 scales), with
  *                         oracle_e4m3_to_f32 the OCP E4M3 decode
+ *   oracle_qwen3_rope     crates/omni-qwen3/kernels/qwen3.cu:64-103 (rope_kv, qwen3_rope)
+ *   oracle_qwen3_rope_dense  qwen3.cu:105-111 (qwen3_rope_dense)
+ *   oracle_hidream_qk_rope   crates/omni-hidream-o1/kernels/hidream.cu:55-106
+ *   oracle_lm_rope        crates/omni-personaplex/kernels/lm.cu:125-182 (lm_rope) with
+ *                         attend.cuh:108-128 (rope_head); oracle_f32_to_e4m3 the
+ *                         OCP E4M3 encode (round to nearest even, saturating)
  *   oracle_fill_normal_bf16 / oracle_splitmix64  the synthetic-input rule
  *
  * Arithmetic follows the reference kernels: f32 accumulation, per-tile online
@@ -451,4 +457,152 @@ int oracle_lm_attend_fp8(const bf16_t* qkv, const uint8_t* kv, const int32_t* po
   fp8_args a = {qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, scale, context > 0 ? context : 0x7fffffff};
   run_items(fp8_item, &a, (int64_t)rows * heads, nthreads);
   return 0;
+}
+
+/* ------------------------------------------- rotary embedding + K/V scatter */
+
+/* f32 -> OCP E4M3, round to nearest even, saturating to +-448 (the finite
+ * range); NaN -> 0x7F with the sign. Derived from the format: 1 sign, 4
+ * exponent bits with bias 7, 3 mantissa bits, subnormals of 2^-9 steps. */
+uint8_t oracle_f32_to_e4m3(float x) {
+  const uint8_t sign = signbit(x) ? 0x80 : 0;
+  if (isnan(x)) return sign | 0x7F;
+  const float a = fabsf(x);
+  if (a >= 448.f) return sign | 0x7E;
+  if (a < ldexpf(1.f, -6)) {  /* subnormal: multiples of 2^-9 */
+    const float m = nearbyintf(ldexpf(a, 9)); /* 0 .. 8; 8 is the smallest normal */
+    return sign | (uint8_t)m;
+  }
+  int e;
+  frexpf(a, &e); /* a = f * 2^e, f in [0.5, 1): the leading bit is 2^(e-1) */
+  e -= 1;
+  float m = nearbyintf(ldexpf(a, 3 - e)); /* 8 .. 16 */
+  if (m == 16.f) {
+    m = 8.f;
+    e += 1;
+  }
+  if (e > 8) return sign | 0x7E;
+  return sign | (uint8_t)(((e + 7) << 3) | ((int)m - 8));
+}
+
+/* One head of rope_kv / hidream_qk_rope: RMSNorm (f32 sum, x * rsqrt rounded
+ * to bf16, times the bf16 weight), then the half-split rotation of pair i
+ * (elements i, i + 64) by pos_of[i] * theta^(-2i/128), rounded to bf16. */
+static void norm_rope_head(const bf16_t* src, bf16_t* dst, const bf16_t* w, const int* pos_of, float eps,
+                           float theta) {
+  float x[HEAD];
+  float ss = 0.f;
+  for (int i = 0; i < HEAD; ++i) {
+    x[i] = bf2f(src[i]);
+    ss += x[i] * x[i];
+  }
+  const float r = 1.f / sqrtf(ss / HEAD + eps);
+  float v[HEAD];
+  for (int i = 0; i < HEAD; ++i) v[i] = bf2f(f2bf(x[i] * r)) * bf2f(w[i]);
+  for (int i = 0; i < HEAD / 2; ++i) {
+    const float inv_freq = 1.f / powf(theta, (float)(2 * i) / HEAD);
+    const float ang = (float)pos_of[i] * inv_freq;
+    const float sn = sinf(ang), cs = cosf(ang);
+    const float a = v[i], b = v[HEAD / 2 + i];
+    dst[i] = f2bf(a * cs - b * sn);
+    dst[HEAD / 2 + i] = f2bf(b * cs + a * sn);
+  }
+}
+
+static void rope_row(bf16_t* qkv, int64_t ld, const bf16_t* q_norm, const bf16_t* k_norm, int n, const int* pos_of,
+                     bf16_t* kdst, int64_t kstride, bf16_t* vdst, int64_t vstride, int hq, int hk, float eps,
+                     float theta) {
+  bf16_t* row = qkv + (int64_t)n * ld;
+  for (int h = 0; h < hq; ++h) norm_rope_head(row + h * HEAD, row + h * HEAD, q_norm, pos_of, eps, theta);
+  for (int h = 0; h < hk; ++h) {
+    norm_rope_head(row + (int64_t)(hq + h) * HEAD, kdst + h * kstride, k_norm, pos_of, eps, theta);
+    memcpy(vdst + h * vstride, row + (int64_t)(hq + hk + h) * HEAD, HEAD * sizeof(bf16_t));
+  }
+}
+
+/* qwen3_rope: q in place, K and V to slot slots[n] of kv [slot][2 hk][128]. */
+void oracle_qwen3_rope(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, const int32_t* pos,
+                       const int32_t* slots, bf16_t* kv, int rows, int hq, int hk, float eps, float theta) {
+  const int64_t ld = (int64_t)(hq + 2 * hk) * HEAD;
+  int pos_of[HEAD / 2];
+  for (int n = 0; n < rows; ++n) {
+    for (int i = 0; i < HEAD / 2; ++i) pos_of[i] = pos[n];
+    bf16_t* k = kv + (int64_t)slots[n] * 2 * hk * HEAD;
+    rope_row(qkv, ld, q_norm, k_norm, n, pos_of, k, HEAD, k + (int64_t)hk * HEAD, HEAD, hq, hk, eps, theta);
+  }
+}
+
+/* qwen3_rope_dense: row n at position base + n % per, slot (n / per) * span + pos. */
+void oracle_qwen3_rope_dense(bf16_t* qkv, const bf16_t* q_norm, const bf16_t* k_norm, bf16_t* kv, int rows, int per,
+                             int base, int span, int hq, int hk, float eps, float theta) {
+  const int64_t ld = (int64_t)(hq + 2 * hk) * HEAD;
+  int pos_of[HEAD / 2];
+  for (int n = 0; n < rows; ++n) {
+    const int p = base + n % per;
+    for (int i = 0; i < HEAD / 2; ++i) pos_of[i] = p;
+    bf16_t* k = kv + ((int64_t)(n / per) * span + p) * 2 * hk * HEAD;
+    rope_row(qkv, ld, q_norm, k_norm, n, pos_of, k, HEAD, k + (int64_t)hk * HEAD, HEAD, hq, hk, eps, theta);
+  }
+}
+
+/* hidream_qk_rope: pair i turns by positions[3n + (i < 3 mrope_hw ? i % 3 : 0)];
+ * K and V to row slots[n] of the caches [slots][hk][128]. */
+void oracle_hidream_qk_rope(bf16_t* qkv, int ld, const bf16_t* q_norm, const bf16_t* k_norm, const int32_t* positions,
+                            const int32_t* slots, bf16_t* k_cache, bf16_t* v_cache, int rows, int hq, int hk,
+                            int mrope_hw, float eps, float theta) {
+  int pos_of[HEAD / 2];
+  for (int n = 0; n < rows; ++n) {
+    for (int i = 0; i < HEAD / 2; ++i) pos_of[i] = positions[3 * (int64_t)n + (i < 3 * mrope_hw ? i % 3 : 0)];
+    const int64_t s = slots[n];
+    rope_row(qkv, ld, q_norm, k_norm, n, pos_of, k_cache + s * hk * HEAD, HEAD, v_cache + s * hk * HEAD, HEAD, hq,
+             hk, eps, theta);
+  }
+}
+
+/* Interleaved rotation of one head: pair (x[2i], x[2i+1]) by pos * exp(i * coef). */
+static void rope_interleaved(const bf16_t* src, float* out, float pos, float coef) {
+  for (int i = 0; i < HEAD / 2; ++i) {
+    const float freq = expf((float)i * coef);
+    const float ang = freq * pos;
+    const float sn = sinf(ang), cs = cosf(ang);
+    const float re = bf2f(src[2 * i]), im = bf2f(src[2 * i + 1]);
+    out[2 * i] = re * cs - im * sn;
+    out[2 * i + 1] = re * sn + im * cs;
+  }
+}
+
+static void quantize_head(const float* x, uint8_t* dst, float* scale) {
+  float amax = 0.f;
+  for (int i = 0; i < HEAD; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  const float sc = fmaxf(amax * (1.f / 448.f), 1e-12f);
+  const float inv = 1.f / sc;
+  for (int i = 0; i < HEAD; ++i) dst[i] = oracle_f32_to_e4m3(x[i] * inv);
+  *scale = sc;
+}
+
+/* lm_rope: q rotated in place (bf16), k rotated then FP8 with its scale, v FP8
+ * with its scale, into slot slots[n] of [K heads | V heads | K scales | V scales]. */
+void oracle_lm_rope(bf16_t* qkv, const int32_t* pos, const int32_t* slots, uint8_t* kv, int rows, int heads,
+                    float coef) {
+  const int64_t slot_bytes = 2LL * heads * HEAD + 2LL * heads * 4;
+  float x[HEAD];
+  for (int n = 0; n < rows; ++n) {
+    bf16_t* row = qkv + (int64_t)n * 3 * heads * HEAD;
+    const float p = (float)pos[n];
+    uint8_t* slot = kv + (int64_t)slots[n] * slot_bytes;
+    float* scales = (float*)(slot + 2LL * heads * HEAD);
+    for (int h = 0; h < heads; ++h) {
+      rope_interleaved(row + h * HEAD, x, p, coef);
+      for (int i = 0; i < HEAD; ++i) row[h * HEAD + i] = f2bf(x[i]);
+    }
+    for (int h = 0; h < heads; ++h) {
+      rope_interleaved(row + (int64_t)(heads + h) * HEAD, x, p, coef);
+      quantize_head(x, slot + (int64_t)h * HEAD, &scales[h]);
+    }
+    for (int h = 0; h < heads; ++h) {
+      const bf16_t* v = row + (int64_t)(2 * heads + h) * HEAD;
+      for (int i = 0; i < HEAD; ++i) x[i] = bf2f(v[i]);
+      quantize_head(x, slot + (int64_t)(heads + h) * HEAD, &scales[heads + h]);
+    }
+  }
 }

@@ -14,6 +14,9 @@ the pega-omni tree):
 * :func:`dense_attend`  — ``crates/omni-hidream-o1/kernels/hidream.cu:209-347``.
 * :func:`lm_attend_fp8` — ``crates/omni-personaplex/kernels/lm.cu:196-290`` (FP8 E4M3 slots).
 * :func:`gather_kv` / :func:`slot` — ``qwen3.cu:210-214`` (``PagedSlots``).
+* :func:`qwen3_rope` / :func:`qwen3_rope_dense` — ``qwen3.cu:64-111``.
+* :func:`hidream_qk_rope` — ``crates/omni-hidream-o1/kernels/hidream.cu:55-106``.
+* :func:`lm_rope` / :func:`f32_to_e4m3` — ``crates/omni-personaplex/kernels/lm.cu:125-182``.
 """
 from __future__ import annotations
 
@@ -56,6 +59,16 @@ def lib():
         L.oracle_e4m3_to_f32.restype = ctypes.c_float
         L.oracle_lm_attend_fp8.argtypes = [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, i32, i32]
         L.oracle_lm_attend_fp8.restype = i32
+        L.oracle_f32_to_e4m3.argtypes = [f32]
+        L.oracle_f32_to_e4m3.restype = ctypes.c_uint8
+        L.oracle_qwen3_rope.argtypes = [P, P, P, P, P, P, i32, i32, i32, f32, f32]
+        L.oracle_qwen3_rope.restype = None
+        L.oracle_qwen3_rope_dense.argtypes = [P, P, P, P, i32, i32, i32, i32, i32, i32, f32, f32]
+        L.oracle_qwen3_rope_dense.restype = None
+        L.oracle_hidream_qk_rope.argtypes = [P, i32, P, P, P, P, P, P, i32, i32, i32, i32, f32, f32]
+        L.oracle_hidream_qk_rope.restype = None
+        L.oracle_lm_rope.argtypes = [P, P, P, P, i32, i32, f32]
+        L.oracle_lm_rope.restype = None
         _lib = L
     return _lib
 
@@ -138,3 +151,36 @@ def gather_kv(kv, hk, indptr, pages, page, s, length):
 
 def slot(indptr, pages, s, t, page) -> int:
     return int(lib().oracle_slot(_p(indptr), _p(pages), s, t, page))
+
+
+def f32_to_e4m3(x: float) -> int:
+    return int(lib().oracle_f32_to_e4m3(float(x)))
+
+
+def qwen3_rope(qkv, q_norm, k_norm, pos, slots, kv, hq, hk, eps, theta):
+    """In place on copies: returns (qkv', kv') after qwen3_rope."""
+    qkv, kv = qkv.copy(), kv.copy()
+    lib().oracle_qwen3_rope(_p(qkv), _p(q_norm), _p(k_norm), _p(pos), _p(slots), _p(kv), int(pos.shape[0]), hq, hk,
+                            float(eps), float(theta))
+    return qkv, kv
+
+
+def qwen3_rope_dense(qkv, q_norm, k_norm, kv, rows, per, base, span, hq, hk, eps, theta):
+    qkv, kv = qkv.copy(), kv.copy()
+    lib().oracle_qwen3_rope_dense(_p(qkv), _p(q_norm), _p(k_norm), _p(kv), rows, per, base, span, hq, hk, float(eps),
+                                  float(theta))
+    return qkv, kv
+
+
+def hidream_qk_rope(qkv, ld, q_norm, k_norm, positions, slots, k_cache, v_cache, hq, hk, mrope_hw, eps, theta):
+    qkv, k_cache, v_cache = qkv.copy(), k_cache.copy(), v_cache.copy()
+    lib().oracle_hidream_qk_rope(_p(qkv), ld, _p(q_norm), _p(k_norm), _p(positions), _p(slots), _p(k_cache),
+                                 _p(v_cache), int(slots.shape[0]), hq, hk, mrope_hw, float(eps), float(theta))
+    return qkv, k_cache, v_cache
+
+
+def lm_rope(qkv, pos, slots, kv, heads, coef):
+    """kv: uint8 [slots][slot_bytes]. Returns (qkv', kv')."""
+    qkv, kv = qkv.copy(), kv.copy()
+    lib().oracle_lm_rope(_p(qkv), _p(pos), _p(slots), _p(kv), int(pos.shape[0]), heads, float(coef))
+    return qkv, kv

@@ -337,3 +337,131 @@ int omni_hidream_attend(const void* q, const void* k, const void* v, void* out, 
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------ rotary + scatter
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int rope_common(omni::RopeArgs& a, int mode, const char* who, void* stream) {
+  if (a.rows < 0) return fail(OMNI_ATTN_EINVAL, "%s: rows=%d", who, a.rows);
+  if (a.hq <= 0 || a.hk <= 0) return fail(OMNI_ATTN_EINVAL, "%s: hq=%d hk=%d", who, a.hq, a.hk);
+  if ((int64_t)a.hq + 2LL * a.hk > 65535 * 16LL) return fail(OMNI_ATTN_EUNSUPPORTED, "%s: too many heads", who);
+  if (a.rows == 0) return ok();
+  if (!a.qkv || !aligned16(a.qkv)) return fail(OMNI_ATTN_EINVAL, "%s: qkv must be a 16-byte aligned device pointer", who);
+  if (a.ld % 8 != 0) return fail(OMNI_ATTN_EINVAL, "%s: row stride %lld is not a multiple of 8", who, (long long)a.ld);
+  const int rc = omni::launch_rope(a, mode, as_stream(stream));
+  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "%s: mode not implemented", who);
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(omni::g_launch_status));
+  return ok();
+}
+
+int norm_rope_checks(const void* q_norm, const void* k_norm, float eps, float theta, const char* who) {
+  if (!q_norm || !k_norm || !aligned16(q_norm) || !aligned16(k_norm))
+    return fail(OMNI_ATTN_EINVAL, "%s: q_norm / k_norm must be 16-byte aligned device pointers", who);
+  if (!std::isfinite(eps) || eps < 0.f || !std::isfinite(theta) || theta <= 0.f)
+    return fail(OMNI_ATTN_EINVAL, "%s: eps=%g theta=%g", who, (double)eps, (double)theta);
+  return 0;
+}
+
+}  // namespace
+
+int omni_qwen3_rope(void* qkv, const void* q_norm, const void* k_norm, const int32_t* pos, const int32_t* slots,
+                    void* kv, int rows, int hq, int hk, float eps, float theta, void* stream) {
+  if (rows > 0) {
+    if (int rc = norm_rope_checks(q_norm, k_norm, eps, theta, "qwen3_rope")) return rc;
+    if (!pos || !slots || !kv || !aligned16(kv)) return fail(OMNI_ATTN_EINVAL, "qwen3_rope: null or misaligned pointer");
+  }
+  omni::RopeArgs a{};
+  a.qkv = static_cast<omni::bf16_t*>(qkv);
+  a.ld = (int64_t)(hq + 2 * hk) * OMNI_ATTN_HEAD_DIM;
+  a.q_norm = static_cast<const omni::bf16_t*>(q_norm);
+  a.k_norm = static_cast<const omni::bf16_t*>(k_norm);
+  a.pos = pos;
+  a.slots = slots;
+  a.kv = static_cast<omni::bf16_t*>(kv);
+  a.rows = rows;
+  a.hq = hq;
+  a.hk = hk;
+  a.eps = eps;
+  a.theta = theta;
+  return rope_common(a, omni::kRopeQwen3, "qwen3_rope", stream);
+}
+
+int omni_qwen3_rope_dense(void* qkv, const void* q_norm, const void* k_norm, void* kv, int rows, int per, int base,
+                          int span, int hq, int hk, float eps, float theta, void* stream) {
+  if (rows > 0) {
+    if (int rc = norm_rope_checks(q_norm, k_norm, eps, theta, "qwen3_rope_dense")) return rc;
+    if (!kv || !aligned16(kv)) return fail(OMNI_ATTN_EINVAL, "qwen3_rope_dense: null or misaligned kv");
+    if (per <= 0 || base < 0 || (int64_t)base + per > span)
+      return fail(OMNI_ATTN_EINVAL, "qwen3_rope_dense: per=%d base=%d span=%d (need base + per <= span)", per, base,
+                  span);
+  }
+  omni::RopeArgs a{};
+  a.qkv = static_cast<omni::bf16_t*>(qkv);
+  a.ld = (int64_t)(hq + 2 * hk) * OMNI_ATTN_HEAD_DIM;
+  a.q_norm = static_cast<const omni::bf16_t*>(q_norm);
+  a.k_norm = static_cast<const omni::bf16_t*>(k_norm);
+  a.kv = static_cast<omni::bf16_t*>(kv);
+  a.rows = rows;
+  a.hq = hq;
+  a.hk = hk;
+  a.per = per;
+  a.base = base;
+  a.span = span;
+  a.eps = eps;
+  a.theta = theta;
+  return rope_common(a, omni::kRopeQwen3Dense, "qwen3_rope_dense", stream);
+}
+
+int omni_lm_rope(void* qkv, const int32_t* pos, const int32_t* slots, void* kv, int rows, int heads, float coef,
+                 void* stream) {
+  if (rows > 0) {
+    if (!pos || !slots || !kv || (reinterpret_cast<uintptr_t>(kv) & 7) != 0)
+      return fail(OMNI_ATTN_EINVAL, "lm_rope: null pointer or kv not 8-byte aligned");
+    if (!std::isfinite(coef)) return fail(OMNI_ATTN_EINVAL, "lm_rope: non-finite coef");
+  }
+  omni::RopeArgs a{};
+  a.qkv = static_cast<omni::bf16_t*>(qkv);
+  a.ld = 3LL * heads * OMNI_ATTN_HEAD_DIM;
+  a.pos = pos;
+  a.slots = slots;
+  a.kv_bytes = kv;
+  a.slot_bytes = 2LL * heads * OMNI_ATTN_HEAD_DIM + 2LL * heads * 4;
+  a.rows = rows;
+  a.hq = heads;
+  a.hk = heads;
+  a.coef = coef;
+  return rope_common(a, omni::kRopeLm, "lm_rope", stream);
+}
+
+int omni_hidream_qk_rope(void* qkv, int ld, const void* q_norm, const void* k_norm, const int32_t* positions,
+                         const int32_t* slots, void* k_cache, void* v_cache, int rows, int hq, int hk, int mrope_hw,
+                         float eps, float theta, void* stream) {
+  if (rows > 0) {
+    if (int rc = norm_rope_checks(q_norm, k_norm, eps, theta, "hidream_qk_rope")) return rc;
+    if (!positions || !slots || !k_cache || !v_cache || !aligned16(k_cache) || !aligned16(v_cache))
+      return fail(OMNI_ATTN_EINVAL, "hidream_qk_rope: null or misaligned pointer");
+    if ((int64_t)ld < (int64_t)(hq + 2 * hk) * OMNI_ATTN_HEAD_DIM)
+      return fail(OMNI_ATTN_EINVAL, "hidream_qk_rope: ld=%d shorter than a [q | k | v] row", ld);
+    if (mrope_hw < 0 || 3 * mrope_hw > OMNI_ATTN_HEAD_DIM / 2)
+      return fail(OMNI_ATTN_EINVAL, "hidream_qk_rope: mrope_hw=%d outside [0, 21]", mrope_hw);
+  }
+  omni::RopeArgs a{};
+  a.qkv = static_cast<omni::bf16_t*>(qkv);
+  a.ld = ld;
+  a.q_norm = static_cast<const omni::bf16_t*>(q_norm);
+  a.k_norm = static_cast<const omni::bf16_t*>(k_norm);
+  a.pos = positions;
+  a.slots = slots;
+  a.k_cache = static_cast<omni::bf16_t*>(k_cache);
+  a.v_cache = static_cast<omni::bf16_t*>(v_cache);
+  a.rows = rows;
+  a.hq = hq;
+  a.hk = hk;
+  a.mrope_hw = mrope_hw;
+  a.eps = eps;
+  a.theta = theta;
+  return rope_common(a, omni::kRopeHidream, "hidream_qk_rope", stream);
+}

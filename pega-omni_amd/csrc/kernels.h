@@ -71,6 +71,27 @@ struct TiledArgs {
 constexpr int kTiledRows = 128;  // packed (position, head) query rows per MFMA tile
 
 int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream);
+
+// Rotary embedding + K/V scatter (the step before attention).
+struct RopeArgs {
+  bf16_t* qkv;
+  int64_t ld;  // elements between qkv rows
+  const bf16_t* q_norm;
+  const bf16_t* k_norm;
+  const int32_t* pos;    // [rows], or [rows][3] (t, h, w) for M-RoPE
+  const int32_t* slots;  // [rows] cache slot of each row
+  bf16_t* kv;            // bf16 slots [2 hk][128]
+  void* kv_bytes;        // FP8 slots of slot_bytes
+  int64_t slot_bytes;
+  bf16_t* k_cache;  // M-RoPE: separate caches [slots][hk][128]
+  bf16_t* v_cache;
+  int rows, hq, hk;
+  int per, base, span;  // dense rows: seq n / per at position base + n % per, slot seq * span + pos
+  int mrope_hw;
+  float eps, theta, coef;
+};
+constexpr int kRopeQwen3 = 0, kRopeQwen3Dense = 1, kRopeHidream = 2, kRopeLm = 3;
+int launch_rope(const RopeArgs& a, int mode, hipStream_t stream);
 int launch_dit(const TiledArgs& a, int batch, hipStream_t stream);
 
 }  // namespace omni

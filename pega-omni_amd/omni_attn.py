@@ -37,6 +37,10 @@ EXPORTS = (
     "omni_attn_prefill_run",
     "omni_hidream_attend",
     "omni_hidream_attend_batched",
+    "omni_qwen3_rope",
+    "omni_qwen3_rope_dense",
+    "omni_lm_rope",
+    "omni_hidream_qk_rope",
     "omni_attn_version",
     "omni_attn_last_error",
 )
@@ -104,6 +108,10 @@ def load(path: str = LIB_PATH):
         "omni_attn_prefill_run": [pplan, P, P, P, P, P, P, P, f32, P, P],
         "omni_hidream_attend": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, P],
         "omni_hidream_attend_batched": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, i32, i64, i64, i64, P],
+        "omni_qwen3_rope": [P, P, P, P, P, P, i32, i32, i32, f32, f32, P],
+        "omni_qwen3_rope_dense": [P, P, P, P, i32, i32, i32, i32, i32, i32, f32, f32, P],
+        "omni_lm_rope": [P, P, P, P, i32, i32, f32, P],
+        "omni_hidream_qk_rope": [P, i32, P, P, P, P, P, P, i32, i32, i32, i32, f32, f32, P],
         "omni_attn_version": [],
         "omni_attn_last_error": [],
     }
@@ -291,3 +299,45 @@ def hidream_attend_batched(q, k, v, out, q_len, kv_len_at, q_stride, causal, sca
                                               int(causal), float(scale_log2), hq, hk, batch, q_bstride, kv_bstride,
                                               out_bstride, _stream(stream)))
     return out
+
+
+# ------------------------------------------------ rotary embedding + K/V scatter
+def qwen3_rope(qkv, q_norm, k_norm, pos, slots, kv, rows, hq, hk, eps, theta, stream=None):
+    """``qwen3_rope`` (crates/omni-qwen3/kernels/qwen3.cu:64-103): q rotated in
+    place, K and V written to slot ``slots[n]`` of the bf16 paged cache."""
+    for t, n in ((qkv, "qkv"), (q_norm, "q_norm"), (k_norm, "k_norm"), (kv, "kv")):
+        _bf16_dev(t, n)
+    _i32_dev(pos, "pos"), _i32_dev(slots, "slots")
+    _check(load().omni_qwen3_rope(_ptr(qkv), _ptr(q_norm), _ptr(k_norm), _ptr(pos), _ptr(slots), _ptr(kv), rows, hq,
+                                  hk, float(eps), float(theta), _stream(stream)))
+
+
+def qwen3_rope_dense(qkv, q_norm, k_norm, kv, rows, per, base, span, hq, hk, eps, theta, stream=None):
+    """``qwen3_rope_dense`` (qwen3.cu:105-111)."""
+    for t, n in ((qkv, "qkv"), (q_norm, "q_norm"), (k_norm, "k_norm"), (kv, "kv")):
+        _bf16_dev(t, n)
+    _check(load().omni_qwen3_rope_dense(_ptr(qkv), _ptr(q_norm), _ptr(k_norm), _ptr(kv), rows, per, base, span, hq,
+                                        hk, float(eps), float(theta), _stream(stream)))
+
+
+def lm_rope(qkv, pos, slots, kv, rows, heads, coef, stream=None):
+    """``lm_rope`` (crates/omni-personaplex/kernels/lm.cu:125-182): kv is a
+    uint8 device tensor of FP8 slots."""
+    import torch
+
+    _bf16_dev(qkv, "qkv"), _i32_dev(pos, "pos"), _i32_dev(slots, "slots")
+    if kv.dtype != torch.uint8 or not kv.is_cuda or not kv.is_contiguous():
+        raise OmniAttnError(EINVAL, "kv must be a contiguous uint8 device tensor of FP8 slots")
+    _check(load().omni_lm_rope(_ptr(qkv), _ptr(pos), _ptr(slots), _ptr(kv), rows, heads, float(coef),
+                               _stream(stream)))
+
+
+def hidream_qk_rope(qkv, ld, q_norm, k_norm, positions, slots, k_cache, v_cache, rows, hq, hk, mrope_hw, eps, theta,
+                    stream=None):
+    """``hidream_qk_rope`` (crates/omni-hidream-o1/kernels/hidream.cu:55-106)."""
+    for t, n in ((qkv, "qkv"), (q_norm, "q_norm"), (k_norm, "k_norm"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _bf16_dev(t, n)
+    _i32_dev(positions, "positions"), _i32_dev(slots, "slots")
+    _check(load().omni_hidream_qk_rope(_ptr(qkv), ld, _ptr(q_norm), _ptr(k_norm), _ptr(positions), _ptr(slots),
+                                       _ptr(k_cache), _ptr(v_cache), rows, hq, hk, mrope_hw, float(eps),
+                                       float(theta), _stream(stream)))

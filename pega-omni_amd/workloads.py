@@ -247,3 +247,79 @@ def fp8_kv_bytes(case) -> int:
     qo = case.rows * case.hq * HEAD * 2 * 2
     idx = int(np.ceil(ln / case.page).sum()) * 4 + 4 * len(case.indptr) + 4 * case.rows
     return kvb + qo + idx
+
+
+# ------------------------------------------- rotary embedding + K/V scatter
+@dataclass
+class RopeCase:
+    """Rows entering rope + scatter: qkv bf16 rows, norm weights, positions,
+    the slot of each row, and the cache they scatter into (pre-filled with
+    random bytes, so a test sees which slots were written)."""
+    kind: str            # "qwen3", "dense", "hidream", "lm"
+    rows: int
+    hq: int
+    hk: int
+    qkv: np.ndarray      # uint16 [rows][ld]
+    ld: int
+    q_norm: np.ndarray | None
+    k_norm: np.ndarray | None
+    pos: np.ndarray      # int32 [rows] or [rows][3]
+    slots: np.ndarray | None
+    cache: dict          # name -> array (kv / k_cache, v_cache)
+    eps: float = 1e-6
+    theta: float = 1e6
+    coef: float = 0.0
+    mrope_hw: int = 20
+    per: int = 0
+    base: int = 0
+    span: int = 0
+
+    def bytes_moved(self) -> int:
+        """Algorithmic HBM bytes of one launch: qkv read once, q written back,
+        K and V (or their FP8 bytes and scales) written, weights and indices."""
+        heads = self.hq + 2 * self.hk
+        rd = self.rows * heads * HEAD * 2
+        if self.kind == "lm":
+            wr = self.rows * (self.hq * HEAD * 2 + 2 * self.hk * (HEAD + 4))
+        else:
+            wr = self.rows * heads * HEAD * 2
+        idx = self.rows * 4 * (3 if self.kind == "hidream" else 2)
+        return rd + wr + idx + (0 if self.kind == "lm" else 2 * HEAD * 2)
+
+
+def rope_case(kind, rows, hq, hk, pool_slots=None, seed=0, pos_hi=4096, ld_pad=0, per=0, base=0, span=0):
+    rng = np.random.default_rng(seed)
+    if kind == "lm":
+        hk = hq
+    ld = (hq + 2 * hk) * HEAD + ld_pad
+    qkv = normal_bits(rng, (rows, ld))
+    q_norm = k_norm = None
+    if kind != "lm":
+        q_norm = f32_to_bf16_bits(1.0 + 0.2 * rng.standard_normal(HEAD, dtype=np.float32))
+        k_norm = f32_to_bf16_bits(1.0 + 0.2 * rng.standard_normal(HEAD, dtype=np.float32))
+    if kind == "hidream":
+        pos = rng.integers(0, pos_hi, size=(rows, 3)).astype(np.int32)
+    else:
+        pos = rng.integers(0, pos_hi, size=rows).astype(np.int32)
+    pool = pool_slots or max(2 * rows, 16)
+    slots = rng.permutation(pool)[:rows].astype(np.int32)
+    case = RopeCase(kind=kind, rows=rows, hq=hq, hk=hk, qkv=qkv, ld=ld, q_norm=q_norm, k_norm=k_norm, pos=pos,
+                    slots=slots, cache={})
+    if kind == "qwen3":
+        case.cache["kv"] = normal_bits(rng, (pool, 2 * hk * HEAD))
+    elif kind == "dense":
+        nseq = (rows + per - 1) // per
+        case.per, case.base, case.span = per, base, span
+        case.pos = (base + np.arange(rows) % per).astype(np.int32)
+        case.slots = None
+        case.cache["kv"] = normal_bits(rng, (nseq * span, 2 * hk * HEAD))
+    elif kind == "hidream":
+        case.cache["k_cache"] = normal_bits(rng, (pool, hk * HEAD))
+        case.cache["v_cache"] = normal_bits(rng, (pool, hk * HEAD))
+    elif kind == "lm":
+        case.cache["kv"] = rng.integers(0, 256, size=(pool, fp8_slot_bytes(hq)), dtype=np.uint8)
+        case.coef = float(np.float32(-np.log(10000.0) * 2.0 / HEAD))
+        case.theta = 10000.0
+    else:
+        raise ValueError(kind)
+    return case

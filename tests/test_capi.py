@@ -141,3 +141,21 @@ def test_prefill_plan_breaks_runs_at_position_gaps():
     pos = np.array([5, 6, 8, 0, 1, 9, 10], np.int32)
     _, work = _plan_host(7, 4, 4, seq, pos)
     assert [tuple(w) for w in work] == [(0, 5, 2, 11), (0, 2, 1, 9), (0, 0, 2, 7), (1, 3, 2, 2)]
+
+
+def test_rope_entry_points_validate_before_launch():
+    L = oa.load()
+    f = ctypes.c_void_p(4096)  # aligned fake device pointer: every call below fails before any launch
+    bad = ctypes.c_void_p(4098)
+    assert L.omni_qwen3_rope(f, f, f, f, f, f, 0, 16, 8, 1e-6, 1e6, None) == oa.OK  # no rows: nothing to do
+    assert L.omni_qwen3_rope(bad, f, f, f, f, f, 4, 16, 8, 1e-6, 1e6, None) == oa.EINVAL
+    assert L.omni_qwen3_rope(f, f, f, None, f, f, 4, 16, 8, 1e-6, 1e6, None) == oa.EINVAL
+    assert L.omni_qwen3_rope(f, f, f, f, f, f, 4, 16, 8, 1e-6, -1.0, None) == oa.EINVAL
+    assert L.omni_qwen3_rope(f, f, f, f, f, f, 4, 0, 8, 1e-6, 1e6, None) == oa.EINVAL
+    assert L.omni_qwen3_rope_dense(f, f, f, f, 10, 5, 3, 7, 16, 8, 1e-6, 1e6, None) == oa.EINVAL  # base+per > span
+    assert L.omni_qwen3_rope_dense(f, f, f, f, 10, 0, 3, 70, 16, 8, 1e-6, 1e6, None) == oa.EINVAL
+    assert L.omni_lm_rope(f, f, f, ctypes.c_void_p(4100), 4, 32, -0.14, None) == oa.EINVAL  # kv not 8-aligned
+    assert L.omni_lm_rope(f, f, f, f, 4, 32, float("nan"), None) == oa.EINVAL
+    assert L.omni_hidream_qk_rope(f, 128, f, f, f, f, f, f, 4, 4, 2, 20, 1e-6, 1e6, None) == oa.EINVAL  # ld too short
+    assert L.omni_hidream_qk_rope(f, 1024, f, f, f, f, f, f, 4, 4, 2, 22, 1e-6, 1e6, None) == oa.EINVAL
+    assert "mrope_hw" in L.omni_attn_last_error().decode()
