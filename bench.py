@@ -257,6 +257,67 @@ def dit_bench(stream, steps, warmup, hk=8):
                 frac=round(fl / (launch_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
 
+def rope_bench(stream, steps, warmup):
+    """Rotary + K/V scatter, one launch per step, at the engines' shapes:
+    config 2 decode rows (qwen3_rope), a config-3 tick (lm_rope into FP8
+    slots), config 4's prefill rows (qwen3_rope) and both HiDream CFG rows
+    (hidream_qk_rope). Bytes: qkv read, q and K/V written, weights, indices."""
+    import numpy as np
+    import torch
+
+    import omni_attn as oa
+    import workloads as W
+
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+    res = {}
+
+    def run(name, rows, hq, hk, call, bytes_):
+        def step(s, ev):
+            if ev is not None:
+                ev[0][0].record(s)
+            call(s)
+            if ev is not None:
+                ev[0][1].record(s)
+
+        ms, launch_ms = time_steps(step, steps * 5, warmup, stream, per_launch=1)
+        res[name] = dict(rows=rows, heads=f"{hq}q/{hk}kv", bytes=bytes_, launch_us=round(launch_ms * 1e3, 2),
+                         gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1),
+                         frac=round(bytes_ / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+
+    rng = np.random.default_rng(7)
+    w = torch.ones(128, dtype=torch.bfloat16, device="cuda")
+    for name, rows, hq, hk, pool in (("qwen3_rope config2", 64, 16, 8, 16384 * 16),
+                                     ("qwen3_rope config4", 25499, 32, 8, 26000)):
+        qkv = torch.randn(rows, (hq + 2 * hk) * 128, device="cuda", generator=gen).to(torch.bfloat16)
+        kv = torch.empty(pool, 2 * hk * 128, dtype=torch.bfloat16, device="cuda")
+        pos, slots = i32(rng.integers(0, 3000, rows)), i32(rng.permutation(pool)[:rows])
+        c = W.RopeCase("qwen3", rows, hq, hk, None, 0, None, None, None, None, {})
+        run(name, rows, hq, hk, lambda s, qkv=qkv, kv=kv, pos=pos, slots=slots, rows=rows, hq=hq, hk=hk:
+            oa.qwen3_rope(qkv, w, w, pos, slots, kv, rows, hq, hk, 1e-6, 1e6, s), c.bytes_moved())
+        del qkv, kv
+    rows, heads, pool = 128, 32, 128 * 3000
+    qkv = torch.randn(rows, 3 * heads * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    kv8 = torch.empty(pool, W.fp8_slot_bytes(heads), dtype=torch.uint8, device="cuda")
+    pos, slots = i32(rng.integers(0, 3000, rows)), i32(rng.permutation(pool)[:rows])
+    coef = float(np.float32(-np.log(10000.0) * 2.0 / 128))
+    c = W.RopeCase("lm", rows, heads, heads, None, 0, None, None, None, None, {})
+    run("lm_rope config3", rows, heads, heads, lambda s: oa.lm_rope(qkv, pos, slots, kv8, rows, heads, coef, s),
+        c.bytes_moved())
+    del qkv, kv8
+    rows, hq, hk = 2 * 4352, 32, 8
+    ld = (hq + 2 * hk) * 128
+    qkv = torch.randn(rows, ld, device="cuda", generator=gen).to(torch.bfloat16)
+    kc = torch.empty(rows, hk * 128, dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    p3, slots = i32(rng.integers(0, 4352, (rows, 3))), i32(np.arange(rows))
+    c = W.RopeCase("hidream", rows, hq, hk, None, 0, None, None, None, None, {})
+    run("hidream_qk_rope config5", rows, hq, hk,
+        lambda s: oa.hidream_qk_rope(qkv, ld, w, w, p3, slots, kc, vc, rows, hq, hk, 20, 1e-6, 5e6, s),
+        c.bytes_moved())
+    return res
+
+
 def measure_peaks(stream):
     """Measured ceilings on this GPU (libomni_peaks.so): bf16 MFMA TFLOP/s
     (4 independent 32x32x16 chains per wave), v_exp_f32 and v_fma_f32 lane
@@ -329,7 +390,7 @@ def main():
     ap.add_argument("--pools", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots)")
+    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
     args = ap.parse_args()
@@ -387,7 +448,12 @@ def main():
         log(f"[bench] {extra['config3_fp8']}")
         del b8
         torch.cuda.empty_cache()
-    if args.only in (4, 5, 2, 6):
+    if args.only in (0, 7):
+        log("[bench] rotary + K/V scatter")
+        extra["rope"] = rope_bench(stream, args.steps, args.warmup)
+        log(f"[bench] {extra['rope']}")
+        torch.cuda.empty_cache()
+    if args.only in (4, 5, 2, 6, 7):
         print(json.dumps({"extra": extra}), flush=True)
         return
 

@@ -12,14 +12,18 @@
 //     in place and of k, then K and V quantized to FP8 E4M3 per (slot, head)
 //     with scale max(amax / 448, 1e-12) into the row's 8448-byte slot.
 //
-// Layout of the work: a 16-lane DPP row owns one 128-element head, lane c
-// holding elements 8c .. 8c + 7 (one 16-byte load and one 16-byte store), so a
-// 256-thread workgroup covers 16 heads of one row. The RMS sum and the FP8
-// absmax are DPP row reductions; in the half-split rotary the partner of
-// element i (< 64) is element i + 64, held by lane c + 8 in the same slot of
-// its registers, one row_ror:8 DPP move away.
+// Layout of the work: one 256-thread workgroup per row (per row and group of
+// 16 heads when rows are few). Its first 64 threads
+// compute the row's 64 rotary angles (cos, sin) into LDS once; then each
+// 16-lane DPP row takes heads grp, grp + 16, ... of the row, lane c holding
+// elements 8c .. 8c + 7 (one 16-byte load and one 16-byte store). The RMS sum
+// and the FP8 absmax are DPP row reductions; in the half-split rotary the
+// partner of element i (< 64) is element i + 64, held by lane c + 8 in the
+// same slot of its registers, one row_ror:8 DPP move away.
 #include "common.h"
 #include "kernels.h"
+
+#include <algorithm>
 
 namespace omni {
 
@@ -53,16 +57,32 @@ __device__ __forceinline__ uint2 e4m3x8(const float* v) {
   return make_uint2((uint32_t)lo, (uint32_t)hi);
 }
 
-constexpr int kPaged = 0, kDense = 1, kMRope = 2;
+constexpr int kPaged = 0, kDense = 1, kMRope = 2, kLm = 3;
+
+// The row's 64 rotary angles, cos and sin, into LDS: thread i < 64 takes pair
+// i. Every head of the row turns by the same angles, so they are computed once
+// per row (one powf / expf and one sincosf per pair) instead of per head.
+template <int MODE>
+__device__ __forceinline__ void row_angles(const RopeArgs& a, int n, int p, float* s_cos, float* s_sin) {
+  const int i = threadIdx.x;
+  if (i < kHead / 2) {
+    float ang;
+    if constexpr (MODE == kLm) {
+      ang = expf((float)i * a.coef) * (float)p;
+    } else {
+      int pe = p;
+      if constexpr (MODE == kMRope) pe = a.pos[3LL * n + (i < 3 * a.mrope_hw ? i % 3 : 0)];
+      ang = (float)pe * (1.f / powf(a.theta, (float)(2 * i) / kHead));
+    }
+    sincosf(ang, &s_sin[i], &s_cos[i]);
+  }
+  __syncthreads();
+}
 
 template <int MODE>
 __global__ __launch_bounds__(kRopeThreads) void norm_rope(RopeArgs a) {
   const int n = blockIdx.x;
-  const int c = threadIdx.x & 15;
-  const int head = blockIdx.y * kHeadsPerGroup + (threadIdx.x >> 4);
-  if (head >= a.hq + 2 * a.hk) return;  // whole DPP rows leave together
-  bf16_t* row = a.qkv + (int64_t)n * a.ld + (int64_t)head * kHead;
-  const uint4 raw = ldg16(row + 8 * c);
+  const int c = threadIdx.x & 15, grp = threadIdx.x >> 4;
 
   int64_t slot;
   int p = 0;
@@ -73,94 +93,111 @@ __global__ __launch_bounds__(kRopeThreads) void norm_rope(RopeArgs a) {
     slot = a.slots[n];
     if constexpr (MODE == kPaged) p = a.pos[n];
   }
-
-  if (head >= a.hq + a.hk) {  // V: a copy into the slot
-    bf16_t* dst = MODE == kMRope ? a.v_cache + (slot * a.hk + (head - a.hq - a.hk)) * kHead
-                                 : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead;
-    *reinterpret_cast<uint4*>(dst + 8 * c) = raw;
-    return;
-  }
-
-  float x[8];
-  widen8(raw, x);
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-  const float r = rsqrtf(row16_sum(ss) / kHead + a.eps);
-  const bool is_q = head < a.hq;
-  float w[8];
-  widen8(ldg16((is_q ? a.q_norm : a.k_norm) + 8 * c), w);
-  float v[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = round_bf16(x[e] * r) * w[e];
-
-  const bool lo = c < 8;
-  const int32_t* p3 = MODE == kMRope ? a.pos + 3LL * n : nullptr;
-  float o[8];
+  __shared__ float s_cos[kHead / 2], s_sin[kHead / 2];
+  row_angles<MODE>(a, n, p, s_cos, s_sin);
+  // Lane c's pair indices are 8 (c & 7) .. + 7, the same for every head.
+  float cs[8], sn[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float partner = dpp<kRowRor8>(v[e]);
-    const int i = 8 * (c & 7) + e;  // rotary pair index
-    int pe = p;
-    if constexpr (MODE == kMRope) pe = p3[i < 3 * a.mrope_hw ? i % 3 : 0];
-    const float inv_freq = 1.f / powf(a.theta, (float)(2 * i) / kHead);
-    float sn, cs;
-    sincosf((float)pe * inv_freq, &sn, &cs);
-    o[e] = lo ? v[e] * cs - partner * sn : v[e] * cs + partner * sn;
+    cs[e] = s_cos[8 * (c & 7) + e];
+    sn[e] = s_sin[8 * (c & 7) + e];
   }
-  bf16_t* dst = is_q ? row
-                     : (MODE == kMRope ? a.k_cache + (slot * a.hk + (head - a.hq)) * kHead
-                                       : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead);
-  *reinterpret_cast<uint4*>(dst + 8 * c) = pack8(o);
+  float w[2][8];
+  widen8(ldg16(a.q_norm + 8 * c), w[0]);
+  widen8(ldg16(a.k_norm + 8 * c), w[1]);
+  const bool lo = c < 8;
+  const int nh = a.hq + 2 * a.hk;
+  bf16_t* row = a.qkv + (int64_t)n * a.ld;
+
+  // Whole DPP rows take the same trip count.
+  for (int head = blockIdx.y * kHeadsPerGroup + grp; head < nh; head += kHeadsPerGroup * gridDim.y) {
+    const uint4 raw = ldg16(row + (int64_t)head * kHead + 8 * c);
+    if (head >= a.hq + a.hk) {  // V: a copy into the slot
+      bf16_t* dst = MODE == kMRope ? a.v_cache + (slot * a.hk + (head - a.hq - a.hk)) * kHead
+                                   : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead;
+      *reinterpret_cast<uint4*>(dst + 8 * c) = raw;
+      continue;
+    }
+    float x[8];
+    widen8(raw, x);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+    const float r = rsqrtf(row16_sum(ss) / kHead + a.eps);
+    const bool is_q = head < a.hq;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = round_bf16(x[e] * r) * w[is_q ? 0 : 1][e];
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float partner = dpp<kRowRor8>(v[e]);  // element i + 64 for a low lane, i - 64 for a high one
+      o[e] = lo ? v[e] * cs[e] - partner * sn[e] : v[e] * cs[e] + partner * sn[e];
+    }
+    bf16_t* dst = is_q ? row + (int64_t)head * kHead
+                       : (MODE == kMRope ? a.k_cache + (slot * a.hk + (head - a.hq)) * kHead
+                                         : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead);
+    *reinterpret_cast<uint4*>(dst + 8 * c) = pack8(o);
+  }
 }
 
 __global__ __launch_bounds__(kRopeThreads) void lm_rope_fp8(RopeArgs a) {
   const int n = blockIdx.x;
-  const int c = threadIdx.x & 15;
+  const int c = threadIdx.x & 15, grp = threadIdx.x >> 4;
   const int heads = a.hq;
-  const int head = blockIdx.y * kHeadsPerGroup + (threadIdx.x >> 4);
-  if (head >= 3 * heads) return;
-  bf16_t* row = a.qkv + (int64_t)n * a.ld + (int64_t)head * kHead;
-  float x[8];
-  widen8(ldg16(row + 8 * c), x);
-
-  if (head < 2 * heads) {  // q or k: interleaved rotary, pairs i = 4c .. 4c + 3
-    const float p = (float)a.pos[n];
+  __shared__ float s_cos[kHead / 2], s_sin[kHead / 2];
+  row_angles<kLm>(a, n, a.pos[n], s_cos, s_sin);
+  // Interleaved pairs: lane c holds pairs 4c .. 4c + 3 (elements 8c .. 8c + 7).
+  float cs[4], sn[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float freq = expf((float)(4 * c + j) * a.coef);
-      float sn, cs;
-      sincosf(freq * p, &sn, &cs);
-      const float re = x[2 * j], im = x[2 * j + 1];
-      x[2 * j] = re * cs - im * sn;
-      x[2 * j + 1] = re * sn + im * cs;
-    }
-    if (head < heads) {
-      *reinterpret_cast<uint4*>(row + 8 * c) = pack8(x);
-      return;
-    }
+  for (int j = 0; j < 4; ++j) {
+    cs[j] = s_cos[4 * c + j];
+    sn[j] = s_sin[4 * c + j];
   }
-  // K (rotated, unrounded) or V (as read): FP8 with a per-(slot, head) scale.
-  const int kv_head = head - heads;  // K heads 0 .. heads-1, then V heads
-  float amax = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
-  amax = row16_max(amax);
-  const float sc = fmaxf(amax * (1.f / 448.f), 1e-12f);
-  const float inv = 1.f / sc;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] *= inv;
+  bf16_t* row = a.qkv + (int64_t)n * a.ld;
   uint8_t* slot = static_cast<uint8_t*>(a.kv_bytes) + (int64_t)a.slots[n] * a.slot_bytes;
-  *reinterpret_cast<uint2*>(slot + (int64_t)kv_head * kHead + 8 * c) = e4m3x8(x);
-  if (c == 0) reinterpret_cast<float*>(slot + 2LL * heads * kHead)[kv_head] = sc;
+  float* scales = reinterpret_cast<float*>(slot + 2LL * heads * kHead);
+
+  for (int head = blockIdx.y * kHeadsPerGroup + grp; head < 3 * heads; head += kHeadsPerGroup * gridDim.y) {
+    float x[8];
+    widen8(ldg16(row + (int64_t)head * kHead + 8 * c), x);
+    if (head < 2 * heads) {  // q or k: rotate
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float re = x[2 * j], im = x[2 * j + 1];
+        x[2 * j] = re * cs[j] - im * sn[j];
+        x[2 * j + 1] = re * sn[j] + im * cs[j];
+      }
+      if (head < heads) {
+        *reinterpret_cast<uint4*>(row + (int64_t)head * kHead + 8 * c) = pack8(x);
+        continue;
+      }
+    }
+    // K (rotated, unrounded) or V (as read): FP8 with a per-(slot, head) scale.
+    const int kv_head = head - heads;  // K heads 0 .. heads-1, then V heads
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+    amax = row16_max(amax);
+    const float sc = fmaxf(amax * (1.f / 448.f), 1e-12f);
+    const float inv = 1.f / sc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= inv;
+    *reinterpret_cast<uint2*>(slot + (int64_t)kv_head * kHead + 8 * c) = e4m3x8(x);
+    if (c == 0) scales[kv_head] = sc;
+  }
 }
 
 }  // namespace
 
 int launch_rope(const RopeArgs& a, int mode, hipStream_t stream) {
   if (a.rows == 0) return 0;
+  // One workgroup per row, or per (row, 16 heads) when there are few rows, so
+  // that a launch still has about 1024 workgroups; each computes the row's
+  // angle table.
   const int heads = mode == kRopeLm ? 3 * a.hq : a.hq + 2 * a.hk;
-  const dim3 grid(a.rows, (heads + kHeadsPerGroup - 1) / kHeadsPerGroup);
+  const int ysplit = std::max(1, std::min((heads + kHeadsPerGroup - 1) / kHeadsPerGroup, (1024 + a.rows - 1) / a.rows));
+  const dim3 grid(a.rows, ysplit);
   switch (mode) {
     case kRopeQwen3: norm_rope<kPaged><<<grid, kRopeThreads, 0, stream>>>(a); break;
     case kRopeQwen3Dense: norm_rope<kDense><<<grid, kRopeThreads, 0, stream>>>(a); break;
