@@ -97,6 +97,42 @@ int omni_attn_decode_run_lastlen(const void* qkv, const void* kv, const int32_t*
                                  int hk, float scale, const omni_attn_decode_plan* plan, void* workspace,
                                  void* stream);
 
+/* Replaces `qwen3_attend_dense` (crates/omni-qwen3/kernels/qwen3.cu:243-248),
+ * the code predictor's attention over a dense workspace laid out as
+ * omni_qwen3_rope_dense writes it: row n sees keys 0 .. base + n % per at slots
+ * (n / per) * span + t of kv [slot][2 hk][128]. The plan is made with page = 1
+ * and max_len >= base + per. */
+int omni_qwen3_attend_dense(const void* qkv, const void* kv, int per, int base, int span, void* out, int hq, int hk,
+                            float scale, const omni_attn_decode_plan* plan, void* workspace, void* stream);
+
+/* ------------------------------------------------ head-64 ring attentions */
+
+/* One workgroup of 64 per (row, head); rings are a few hundred keys at most.
+ * Head dim 64; qkv rows [3 heads][64]; out rows [heads][64]. Per-session
+ * state lives at state + lines[s] * stride bytes (16-byte aligned). */
+
+/* Replaces `mimi_attend` (crates/omni-personaplex/kernels/mimi.cu:248-263):
+ * row n of session s = n / T at position p = pos[s] * T + n % T sees
+ * len = min(p + 1, context) ring slots (p - len + 1 + t) % context, slots
+ * [2 heads][64] (K heads then V heads). */
+int omni_mimi_attend(const void* qkv, const int32_t* pos, const int32_t* lines, const void* state, void* out, int rows,
+                     int T, int heads, float scale, int context, int64_t stride, void* stream);
+
+/* Replaces `codec_attention` (crates/omni-qwen3-tts/kernels/codec.cu:168-277):
+ * for session r at p = pos[r], q and k turned by the half-split rotary
+ * (pair i = dims i, i + 32, angle p * theta^(-2i/64)) and rounded to bf16; k
+ * and v written to frame p % 72 of the session's ring K[72][heads * 64] then
+ * V[72][heads * 64]; q attends to frames p - n + 1 .. p, n = min(p + 1, 72),
+ * with scale 1/8. */
+int omni_codec_attention(const void* qkv, const int32_t* pos, const int32_t* lines, void* kv, void* out, int rows,
+                         int64_t stride, int heads, float theta, void* stream);
+
+/* Replaces `lm_dep_kv_attend` (crates/omni-personaplex/kernels/lm.cu:314-366):
+ * depformer step `step` (0..7) of session s writes its K and V into ws
+ * [seqs][8][K | V][heads * 64] at that step and attends to steps 0 .. step. */
+int omni_lm_dep_kv_attend(const void* qkv, void* ws, int step, void* out, int rows, int heads, float scale,
+                          void* stream);
+
 /* ---------------------------------------------------------- page tables */
 
 /* Host check of a page table before upload: indptr monotone from 0, every

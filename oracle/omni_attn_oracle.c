@@ -27,6 +27,12 @@
  *   oracle_lm_rope        crates/omni-personaplex/kernels/lm.cu:125-182 (lm_rope) with
  *                         attend.cuh:108-128 (rope_head); oracle_f32_to_e4m3 the
  *                         OCP E4M3 encode (round to nearest even, saturating)
+ *   oracle_qwen3_attend_dense  crates/omni-qwen3/kernels/qwen3.cu:243-248
+ *   oracle_mimi_attend    crates/omni-personaplex/kernels/mimi.cu:248-263 (head 64 ring in
+ *                         the session's state, attend_row<64> of attend.cuh:41-106)
+ *   oracle_codec_attention  crates/omni-qwen3-tts/kernels/codec.cu:168-277 (rotary, 72-frame
+ *                         ring write and attention, fused)
+ *   oracle_lm_dep_kv_attend crates/omni-personaplex/kernels/lm.cu:314-366 (depformer step)
  *   oracle_fill_normal_bf16 / oracle_splitmix64  the synthetic-input rule
  *
  * Arithmetic follows the reference kernels: f32 accumulation, per-tile online
@@ -178,6 +184,7 @@ typedef struct {
   int hq, hk;
   float scale;
   int context;
+  int dense_per, dense_base, dense_span; /* dense_per > 0: qwen3_attend_dense rows */
 } paged_args;
 
 /* One (row n, kv head kh) work item. Restates attend<G> (qwen3.cu:123-208):
@@ -190,8 +197,9 @@ static void paged_item(void* vctx, int64_t item) {
   const int n = (int)(item / a->hk), kh = (int)(item % a->hk);
   const int G = a->hq / a->hk;
   const int s = a->ragged ? a->seq[n] : n;
-  int len = a->pos[n] + 1;
+  int len = a->dense_per > 0 ? a->dense_base + n % a->dense_per + 1 : a->pos[n] + 1;
   if (len > a->context) len = a->context;
+  const int64_t dense_first = a->dense_per > 0 ? (int64_t)(n / a->dense_per) * a->dense_span : 0;
   const int64_t per_slot = 2LL * a->hk * HEAD;
   const bf16_t* q = a->qkv + ((int64_t)n * (a->hq + 2 * a->hk) + (int64_t)kh * G) * HEAD;
   float qs[GMAX][HEAD];
@@ -211,7 +219,8 @@ static void paged_item(void* vctx, int64_t item) {
         for (int lane = 0; lane < LANES; ++lane) {
           const int t = base + lane;
           const int valid = t < len;
-          slot[lane] = oracle_slot(a->indptr, a->pages, s, valid ? t : base, a->page);
+          slot[lane] = a->dense_per > 0 ? dense_first + (valid ? t : base)
+                                        : oracle_slot(a->indptr, a->pages, s, valid ? t : base, a->page);
           const bf16_t* k = a->kv + slot[lane] * per_slot + (int64_t)kh * HEAD;
           float dot = 0.f;
           for (int d = 0; d < HEAD; ++d) dot += qs[g][d] * bf2f(k[d]);
@@ -257,7 +266,17 @@ int oracle_paged_attend(const bf16_t* qkv, const bf16_t* kv, const int32_t* pos,
                         const int32_t* indptr, const int32_t* pages, int page, bf16_t* out, int rows, int hq, int hk,
                         float scale, int context, int nthreads) {
   if (hk <= 0 || hq % hk != 0 || hq / hk > GMAX || page <= 0) return -1;
-  paged_args a = {qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, context > 0 ? context : 0x7fffffff};
+  paged_args a = {qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, context > 0 ? context : 0x7fffffff, 0, 0, 0};
+  run_items(paged_item, &a, (int64_t)rows * hk, nthreads);
+  return 0;
+}
+
+/* qwen3_attend_dense (crates/omni-qwen3/kernels/qwen3.cu:243-248): row n sees
+ * keys 0 .. base + n % per at dense slots (n / per) * span + t of kv. */
+int oracle_qwen3_attend_dense(const bf16_t* qkv, const bf16_t* kv, int per, int base, int span, bf16_t* out, int rows,
+                              int hq, int hk, float scale, int nthreads) {
+  if (hk <= 0 || hq % hk != 0 || hq / hk > GMAX || per <= 0) return -1;
+  paged_args a = {qkv, kv, NULL, NULL, 0, NULL, NULL, 1, out, hq, hk, scale, 0x7fffffff, per, base, span};
   run_items(paged_item, &a, (int64_t)rows * hk, nthreads);
   return 0;
 }
@@ -603,6 +622,182 @@ void oracle_lm_rope(bf16_t* qkv, const int32_t* pos, const int32_t* slots, uint8
       const bf16_t* v = row + (int64_t)(2 * heads + h) * HEAD;
       for (int i = 0; i < HEAD; ++i) x[i] = bf2f(v[i]);
       quantize_head(x, slot + (int64_t)(heads + h) * HEAD, &scales[heads + h]);
+    }
+  }
+}
+
+/* ------------------------------------------------ head-64 ring attentions */
+
+#define D64 64
+
+/* attend_row<64> (attend.cuh:41-106) for one (row, head): q (64 f32), keys
+ * t = 0 .. len-1 with K row krow(t) and V row vrow(t); 4 warps x 32-key tiles,
+ * online softmax with natural exp per tile, warps merged at the end. */
+static void attend_row64(const float* q, const bf16_t* const* krow, const bf16_t* const* vrow, int len, float scale,
+                         bf16_t* out) {
+  float M[WARPS], L[WARPS], O[WARPS][D64];
+  for (int w = 0; w < WARPS; ++w) {
+    float m = -INFINITY, l = 0.f;
+    for (int d = 0; d < D64; ++d) O[w][d] = 0.f;
+    for (int base = w * LANES; base < len; base += WARPS * LANES) {
+      float sv[LANES], p[LANES];
+      float tmax = -INFINITY;
+      for (int lane = 0; lane < LANES; ++lane) {
+        const int t = base + lane;
+        const bf16_t* k = krow[t < len ? t : base];
+        float dot = 0.f;
+        for (int d = 0; d < D64; ++d) dot += q[d] * bf2f(k[d]);
+        sv[lane] = t < len ? dot * scale : -INFINITY;
+        if (sv[lane] > tmax) tmax = sv[lane];
+      }
+      const float m2 = fmaxf(m, tmax);
+      const float corr = expf(m - m2);
+      for (int lane = 0; lane < LANES; ++lane) p[lane] = expf(sv[lane] - m2);
+      l = l * corr + bfly_sum(p);
+      for (int d = 0; d < D64; ++d) O[w][d] *= corr;
+      m = m2;
+      const int count = len - base < LANES ? len - base : LANES;
+      for (int j = 0; j < count; ++j)
+        for (int d = 0; d < D64; ++d) O[w][d] += p[j] * bf2f(vrow[base + j][d]);
+    }
+    M[w] = m;
+    L[w] = l;
+  }
+  float top = -INFINITY;
+  for (int w = 0; w < WARPS; ++w) top = fmaxf(top, M[w]);
+  for (int d = 0; d < D64; ++d) {
+    float num = 0.f, den = 0.f;
+    for (int w = 0; w < WARPS; ++w) {
+      const float e = M[w] == -INFINITY ? 0.f : expf(M[w] - top);
+      num += O[w][d] * e;
+      den += L[w] * e;
+    }
+    out[d] = f2bf(num / den);
+  }
+}
+
+/* mimi_attend: row n of session s = n / T at position p = pos[s] * T + n % T
+ * sees len = min(p + 1, context) ring slots (p - len + 1 + t) % context of the
+ * session's ring at state + lines[s] * stride bytes, slots [2 heads][64]. */
+void oracle_mimi_attend(const bf16_t* qkv, const int32_t* pos, const int32_t* lines, const uint8_t* state,
+                        bf16_t* out, int rows, int T, int heads, float scale, int context, int64_t stride) {
+  const bf16_t** krow = (const bf16_t**)malloc(sizeof(bf16_t*) * (size_t)context);
+  const bf16_t** vrow = (const bf16_t**)malloc(sizeof(bf16_t*) * (size_t)context);
+  float q[D64];
+  for (int n = 0; n < rows; ++n) {
+    const int s = n / T, p = pos[s] * T + n % T;
+    const int len = p + 1 < context ? p + 1 : context;
+    const bf16_t* ring = (const bf16_t*)(state + (int64_t)lines[s] * stride);
+    for (int h = 0; h < heads; ++h) {
+      for (int t = 0; t < len; ++t) {
+        const int64_t slot = (p - len + 1 + t) % context;
+        krow[t] = ring + (slot * 2 * heads + h) * D64;
+        vrow[t] = ring + (slot * 2 * heads + heads + h) * D64;
+      }
+      const bf16_t* qh = qkv + ((int64_t)n * 3 * heads + h) * D64;
+      for (int d = 0; d < D64; ++d) q[d] = bf2f(qh[d]);
+      attend_row64(q, krow, vrow, len, scale, out + ((int64_t)n * heads + h) * D64);
+    }
+  }
+  free(krow);
+  free(vrow);
+}
+
+#define CODEC_WINDOW 72
+
+/* codec_attention for session r, head h: q and k turned by the half-split
+ * rotary at p = pos[r] (pair i = elements i, i + 32, angle p * theta^(-2i/64))
+ * and rounded to bf16; k and v written to frame p % 72 of the ring at
+ * kv + lines[r] * stride bytes (K[72][heads * 64] then V[72][heads * 64]);
+ * then q against frames p - n + 1 .. p, n = min(p + 1, 72), scale 1/8, one
+ * softmax over all n scores (max, sum of exp, then the weighted V rows). */
+void oracle_codec_attention(const bf16_t* qkv, const int32_t* pos, const int32_t* lines, uint8_t* kv, bf16_t* out,
+                            int rows, int64_t stride, int heads, float theta) {
+  const int width = heads * D64;
+  for (int r = 0; r < rows; ++r) {
+    bf16_t* ring = (bf16_t*)(kv + (int64_t)lines[r] * stride);
+    const int p = pos[r];
+    const int n = p + 1 < CODEC_WINDOW ? p + 1 : CODEC_WINDOW;
+    const int64_t vofs = (int64_t)CODEC_WINDOW * width;
+    for (int h = 0; h < heads; ++h) {
+      const bf16_t* row = qkv + (int64_t)r * 3 * width + h * D64;
+      float q[D64];
+      bf16_t krot[D64];
+      for (int w = 0; w < 2; ++w) {
+        const bf16_t* src = row + (int64_t)w * width;
+        for (int i = 0; i < D64 / 2; ++i) {
+          const float inv_freq = 1.f / powf(theta, (float)(2 * i) / D64);
+          const float ang = (float)p * inv_freq;
+          const float sn = sinf(ang), cs = cosf(ang);
+          const float lo = bf2f(src[i]), hi = bf2f(src[i + D64 / 2]);
+          const bf16_t a = f2bf(lo * cs - hi * sn), b = f2bf(hi * cs + lo * sn);
+          if (w == 0) {
+            q[i] = bf2f(a);
+            q[i + D64 / 2] = bf2f(b);
+          } else {
+            krot[i] = a;
+            krot[i + D64 / 2] = b;
+          }
+        }
+      }
+      const int64_t at = (int64_t)(p % CODEC_WINDOW) * width + h * D64;
+      memcpy(ring + at, krot, sizeof krot);
+      memcpy(ring + vofs + at, row + 2LL * width, D64 * sizeof(bf16_t));
+      float sc[CODEC_WINDOW];
+      float m = -INFINITY;
+      const int j0 = p - n + 1;
+      for (int j = 0; j < n; ++j) {
+        const bf16_t* k = ring + (int64_t)((j0 + j) % CODEC_WINDOW) * width + h * D64;
+        float dot = 0.f;
+        for (int d = 0; d < D64; ++d) dot += q[d] * bf2f(k[d]);
+        sc[j] = dot * (1.f / sqrtf((float)D64));
+        if (sc[j] > m) m = sc[j];
+      }
+      float l = 0.f, acc[D64];
+      for (int d = 0; d < D64; ++d) acc[d] = 0.f;
+      for (int j = 0; j < n; ++j) {
+        const float pj = expf(sc[j] - m);
+        l += pj;
+        const bf16_t* v = ring + vofs + (int64_t)((j0 + j) % CODEC_WINDOW) * width + h * D64;
+        for (int d = 0; d < D64; ++d) acc[d] += pj * bf2f(v[d]);
+      }
+      for (int d = 0; d < D64; ++d) out[(int64_t)r * width + h * D64 + d] = f2bf(acc[d] / l);
+    }
+  }
+}
+
+#define DEP_STEPS 8
+
+/* lm_dep_kv_attend for session s, head h at depformer step `step`: K and V of
+ * the row into step `step` of the session's workspace ws[s][8][K | V][heads*64],
+ * then q against steps 0 .. step in order with a running (m, l) updated per key
+ * in natural exp, output acc / l. */
+void oracle_lm_dep_kv_attend(const bf16_t* qkv, bf16_t* ws, int step, bf16_t* out, int seqs, int heads, float scale) {
+  const int width = heads * D64;
+  for (int s = 0; s < seqs; ++s) {
+    const bf16_t* row = qkv + (int64_t)s * 3 * width;
+    const int64_t base = (int64_t)s * DEP_STEPS * 2 * width;
+    for (int h = 0; h < heads; ++h) {
+      memcpy(ws + base + (int64_t)step * 2 * width + h * D64, row + width + h * D64, D64 * sizeof(bf16_t));
+      memcpy(ws + base + (int64_t)step * 2 * width + width + h * D64, row + 2 * width + h * D64,
+             D64 * sizeof(bf16_t));
+    }
+    for (int h = 0; h < heads; ++h) {
+      float m = -INFINITY, l = 0.f, acc[D64];
+      for (int d = 0; d < D64; ++d) acc[d] = 0.f;
+      for (int t = 0; t <= step; ++t) {
+        const bf16_t* k = ws + base + (int64_t)t * 2 * width + h * D64;
+        const bf16_t* v = k + width;
+        float dot = 0.f;
+        for (int d = 0; d < D64; ++d) dot += bf2f(row[h * D64 + d]) * bf2f(k[d]);
+        const float sc = dot * scale;
+        const float m2 = fmaxf(m, sc);
+        const float corr = expf(m - m2), p = expf(sc - m2);
+        l = l * corr + p;
+        for (int d = 0; d < D64; ++d) acc[d] = acc[d] * corr + p * bf2f(v[d]);
+        m = m2;
+      }
+      for (int d = 0; d < D64; ++d) out[(int64_t)s * width + h * D64 + d] = f2bf(acc[d] * (1.f / l));
     }
   }
 }

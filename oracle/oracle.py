@@ -15,6 +15,10 @@ the pega-omni tree):
 * :func:`lm_attend_fp8` — ``crates/omni-personaplex/kernels/lm.cu:196-290`` (FP8 E4M3 slots).
 * :func:`gather_kv` / :func:`slot` — ``qwen3.cu:210-214`` (``PagedSlots``).
 * :func:`qwen3_rope` / :func:`qwen3_rope_dense` — ``qwen3.cu:64-111``.
+* :func:`qwen3_attend_dense` — ``qwen3.cu:243-248``.
+* :func:`mimi_attend` — ``crates/omni-personaplex/kernels/mimi.cu:248-263``.
+* :func:`codec_attention` — ``crates/omni-qwen3-tts/kernels/codec.cu:168-277``.
+* :func:`lm_dep_kv_attend` — ``crates/omni-personaplex/kernels/lm.cu:314-366``.
 * :func:`hidream_qk_rope` — ``crates/omni-hidream-o1/kernels/hidream.cu:55-106``.
 * :func:`lm_rope` / :func:`f32_to_e4m3` — ``crates/omni-personaplex/kernels/lm.cu:125-182``.
 """
@@ -59,6 +63,14 @@ def lib():
         L.oracle_e4m3_to_f32.restype = ctypes.c_float
         L.oracle_lm_attend_fp8.argtypes = [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, i32, i32]
         L.oracle_lm_attend_fp8.restype = i32
+        L.oracle_qwen3_attend_dense.argtypes = [P, P, i32, i32, i32, P, i32, i32, i32, f32, i32]
+        L.oracle_qwen3_attend_dense.restype = i32
+        L.oracle_mimi_attend.argtypes = [P, P, P, P, P, i32, i32, i32, f32, i32, i64]
+        L.oracle_mimi_attend.restype = None
+        L.oracle_codec_attention.argtypes = [P, P, P, P, P, i32, i64, i32, f32]
+        L.oracle_codec_attention.restype = None
+        L.oracle_lm_dep_kv_attend.argtypes = [P, P, i32, P, i32, i32, f32]
+        L.oracle_lm_dep_kv_attend.restype = None
         L.oracle_f32_to_e4m3.argtypes = [f32]
         L.oracle_f32_to_e4m3.restype = ctypes.c_uint8
         L.oracle_qwen3_rope.argtypes = [P, P, P, P, P, P, i32, i32, i32, f32, f32]
@@ -184,3 +196,36 @@ def lm_rope(qkv, pos, slots, kv, heads, coef):
     qkv, kv = qkv.copy(), kv.copy()
     lib().oracle_lm_rope(_p(qkv), _p(pos), _p(slots), _p(kv), int(pos.shape[0]), heads, float(coef))
     return qkv, kv
+
+
+def qwen3_attend_dense(qkv, kv, per, base, span, hq, hk, scale, nthreads=1):
+    rows = int(qkv.shape[0])
+    out = np.zeros((rows, hq * 128), dtype=np.uint16)
+    if lib().oracle_qwen3_attend_dense(_p(qkv), _p(kv), per, base, span, _p(out), rows, hq, hk, float(scale),
+                                       int(nthreads)) != 0:
+        raise ValueError("oracle_qwen3_attend_dense: unsupported shape")
+    return out
+
+
+def mimi_attend(qkv, pos, lines, state, rows, T, heads, scale, context, stride):
+    """state: uint8 bytes of every session's ring. Returns out uint16 [rows][heads*64]."""
+    out = np.zeros((rows, heads * 64), dtype=np.uint16)
+    lib().oracle_mimi_attend(_p(qkv), _p(pos), _p(lines), _p(state), _p(out), rows, T, heads, float(scale), context,
+                             int(stride))
+    return out
+
+
+def codec_attention(qkv, pos, lines, kv, rows, stride, heads, theta):
+    """Returns (out, kv') with kv' the ring bytes after the frame writes."""
+    kv = kv.copy()
+    out = np.zeros((rows, heads * 64), dtype=np.uint16)
+    lib().oracle_codec_attention(_p(qkv), _p(pos), _p(lines), _p(kv), _p(out), rows, int(stride), heads, float(theta))
+    return out, kv
+
+
+def lm_dep_kv_attend(qkv, ws, step, seqs, heads, scale):
+    """Returns (out, ws')."""
+    ws = ws.copy()
+    out = np.zeros((seqs, heads * 64), dtype=np.uint16)
+    lib().oracle_lm_dep_kv_attend(_p(qkv), _p(ws), step, _p(out), seqs, heads, float(scale))
+    return out, ws

@@ -60,13 +60,14 @@ int pick_chunk(int rows, int hk, int max_len) {
 int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
                   const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
                   int context, int len_mode, const omni_attn_decode_plan* plan, void* workspace, void* stream,
-                  int fp8 = 0) {
+                  int fp8 = 0, int dense_per = 0, int dense_base = 0, int dense_span = 0) {
   if (!plan) return fail(OMNI_ATTN_EINVAL, "decode: null plan");
   if (plan->hq != hq || plan->hk != hk || plan->page != page)
     return fail(OMNI_ATTN_EINVAL, "decode: plan was made for hq=%d hk=%d page=%d, called with hq=%d hk=%d page=%d",
                 plan->hq, plan->hk, plan->page, hq, hk, page);
   if (plan->rows == 0) return ok();
-  if (!qkv || !kv || !pos || !indptr || !pages || !out || (ragged && !seq))
+  const bool dense = len_mode == 2;
+  if (!qkv || !kv || !out || (!dense && (!pos || !indptr || !pages || (ragged && !seq))))
     return fail(OMNI_ATTN_EINVAL, "decode: null device pointer");
   if (plan->splits > 1 && (!workspace || plan->workspace_bytes <= 0))
     return fail(OMNI_ATTN_EWORKSPACE, "decode: plan needs %lld workspace bytes", (long long)plan->workspace_bytes);
@@ -98,6 +99,9 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.fp8 = fp8;
   a.slot_bytes = 2LL * hk * OMNI_ATTN_HEAD_DIM + 2LL * hk * 4;
   a.group_heads = plan->group_heads;
+  a.dense_per = dense_per;
+  a.dense_base = dense_base;
+  a.dense_span = dense_span;
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d not in {1,2,4}", hq / hk);
   if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(omni::g_launch_status));
@@ -464,4 +468,92 @@ int omni_hidream_qk_rope(void* qkv, int ld, const void* q_norm, const void* k_no
   a.eps = eps;
   a.theta = theta;
   return rope_common(a, omni::kRopeHidream, "hidream_qk_rope", stream);
+}
+
+int omni_qwen3_attend_dense(const void* qkv, const void* kv, int per, int base, int span, void* out, int hq, int hk,
+                            float scale, const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  if (per <= 0 || base < 0 || (int64_t)base + per > span)
+    return fail(OMNI_ATTN_EINVAL, "qwen3_attend_dense: per=%d base=%d span=%d (need base + per <= span)", per, base,
+                span);
+  if (plan && plan->max_len < base + per)
+    return fail(OMNI_ATTN_EINVAL, "qwen3_attend_dense: plan max_len=%d below base + per=%d", plan->max_len, base + per);
+  return decode_common(qkv, kv, nullptr, nullptr, 0, nullptr, nullptr, 1, out, hq, hk, scale, 0, 2, plan, workspace,
+                       stream, 0, per, base, span);
+}
+
+// ------------------------------------------------------ head-64 ring attentions
+
+namespace {
+
+int short_common(omni::ShortArgs& a, int kind, const char* who, void* stream) {
+  if (a.rows < 0 || a.heads <= 0) return fail(OMNI_ATTN_EINVAL, "%s: rows=%d heads=%d", who, a.rows, a.heads);
+  if (a.heads > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "%s: heads=%d", who, a.heads);
+  if (a.rows == 0) return ok();
+  if (!a.qkv || !a.out || !aligned16(a.qkv) || !aligned16(a.out))
+    return fail(OMNI_ATTN_EINVAL, "%s: qkv / out must be 16-byte aligned device pointers", who);
+  const int rc = omni::launch_short(a, kind, as_stream(stream));
+  if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "%s: launch failed: %s", who, hipGetErrorString(omni::g_launch_status));
+  return ok();
+}
+
+}  // namespace
+
+int omni_mimi_attend(const void* qkv, const int32_t* pos, const int32_t* lines, const void* state, void* out, int rows,
+                     int T, int heads, float scale, int context, int64_t stride, void* stream) {
+  if (rows > 0) {
+    if (!pos || !lines || !state || !aligned16(state)) return fail(OMNI_ATTN_EINVAL, "mimi_attend: null pointer");
+    if (T <= 0 || context <= 0 || stride % 16 != 0 || !std::isfinite(scale))
+      return fail(OMNI_ATTN_EINVAL, "mimi_attend: T=%d context=%d stride=%lld", T, context, (long long)stride);
+  }
+  omni::ShortArgs a{};
+  a.qkv = static_cast<const omni::bf16_t*>(qkv);
+  a.pos = pos;
+  a.lines = lines;
+  a.state = const_cast<void*>(state);
+  a.stride = stride;
+  a.out = static_cast<omni::bf16_t*>(out);
+  a.rows = rows;
+  a.heads = heads;
+  a.T = T;
+  a.context = context;
+  a.scale = scale;
+  return short_common(a, omni::kShortMimi, "mimi_attend", stream);
+}
+
+int omni_codec_attention(const void* qkv, const int32_t* pos, const int32_t* lines, void* kv, void* out, int rows,
+                         int64_t stride, int heads, float theta, void* stream) {
+  if (rows > 0) {
+    if (!pos || !lines || !kv || !aligned16(kv)) return fail(OMNI_ATTN_EINVAL, "codec_attention: null pointer");
+    if (stride % 16 != 0 || !std::isfinite(theta) || theta <= 0.f)
+      return fail(OMNI_ATTN_EINVAL, "codec_attention: stride=%lld theta=%g", (long long)stride, (double)theta);
+  }
+  omni::ShortArgs a{};
+  a.qkv = static_cast<const omni::bf16_t*>(qkv);
+  a.pos = pos;
+  a.lines = lines;
+  a.state = kv;
+  a.stride = stride;
+  a.out = static_cast<omni::bf16_t*>(out);
+  a.rows = rows;
+  a.heads = heads;
+  a.theta = theta;
+  return short_common(a, omni::kShortCodec, "codec_attention", stream);
+}
+
+int omni_lm_dep_kv_attend(const void* qkv, void* ws, int step, void* out, int rows, int heads, float scale,
+                          void* stream) {
+  if (rows > 0) {
+    if (!ws || !aligned16(ws)) return fail(OMNI_ATTN_EINVAL, "lm_dep_kv_attend: null or misaligned ws");
+    if (step < 0 || step >= 8 || !std::isfinite(scale))
+      return fail(OMNI_ATTN_EINVAL, "lm_dep_kv_attend: step=%d outside [0, 8)", step);
+  }
+  omni::ShortArgs a{};
+  a.qkv = static_cast<const omni::bf16_t*>(qkv);
+  a.ws = static_cast<omni::bf16_t*>(ws);
+  a.out = static_cast<omni::bf16_t*>(out);
+  a.rows = rows;
+  a.heads = heads;
+  a.step = step;
+  a.scale = scale;
+  return short_common(a, omni::kShortDep, "lm_dep_kv_attend", stream);
 }

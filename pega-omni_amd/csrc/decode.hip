@@ -34,8 +34,10 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int n, int s) {
   int len;
   if (a.len_mode == 0)
     len = a.pos[n] + 1;
-  else
+  else if (a.len_mode == 1)
     len = ((a.indptr[s + 1] - a.indptr[s] - 1) << a.page_shift) + a.pos[s];
+  else
+    len = a.dense_base + n % a.dense_per + 1;
   return min(len, a.context);
 }
 
@@ -80,9 +82,13 @@ __device__ __forceinline__ void merge_waves(const DecodeArgs& a, int n, int kh, 
   }
 }
 
-// UP: every group of 4 key rows (page >= 4) lies in one page, so its page id is
-// one wave-uniform scalar load; otherwise each lane loads its own.
-template <int G, bool UP>
+// Where key t of a row lives. kSlotsUniform: every group of 4 key rows
+// (page >= 4) lies in one page, so its page id is one wave-uniform scalar
+// load; kSlotsLane: each lane loads its own page id; kSlotsDense: a dense
+// workspace, slot (n / per) * span + t (qwen3_attend_dense).
+constexpr int kSlotsLane = 0, kSlotsUniform = 1, kSlotsDense = 2;
+
+template <int G, int SLOTS>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
   const int s = a.ragged ? a.seq[n] : n;
@@ -106,7 +112,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
     for (int e = 0; e < 8; ++e) q[g][e] *= a.scale_log2;
   }
 
-  const int32_t* pg = a.pages + a.indptr[s];
+  const int32_t* pg = SLOTS == kSlotsDense ? nullptr : a.pages + a.indptr[s];
+  const int64_t dense_first = SLOTS == kSlotsDense ? (int64_t)(n / a.dense_per) * a.dense_span : 0;
   const int64_t per_slot = 2LL * a.hk * kHead;
   const bf16_t* kb = a.kv + (int64_t)kh * kHead + c * 8;
   const bf16_t* vb = a.kv + (int64_t)(a.hk + kh) * kHead + c * 8;
@@ -125,13 +132,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   // and reads a valid slot). Page ids are loaded one tile ahead, so the K/V
   // loads of a tile never wait on its page-table reads.
   auto page_of = [&](int tb, int i) -> int {
-    if constexpr (UP)
+    if constexpr (SLOTS == kSlotsDense)
+      return 0;
+    else if constexpr (SLOTS == kSlotsUniform)
       return pg[__builtin_amdgcn_readfirstlane(min(tb + 4 * i, t1 - 1) >> shift)];
     else
       return pg[min(tb + 4 * i + r, t1 - 1) >> shift];
   };
   constexpr int kStride = kDecodeWaves * kTileKeys;
-  int pid[8];
+  int pid[8] = {};
   const int tb0 = t0 + wave * kTileKeys;
   if (tb0 < t1) {
 #pragma unroll
@@ -142,7 +151,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int t = min(tb + 4 * i + r, t1 - 1);
-      off[i] = (((int64_t)pid[i] << shift) | (t & pmask)) * per_slot;
+      if constexpr (SLOTS == kSlotsDense)
+        off[i] = (dense_first + t) * per_slot;
+      else
+        off[i] = (((int64_t)pid[i] << shift) | (t & pmask)) * per_slot;
     }
     uint4 kr[8], vr[8];
 #pragma unroll
@@ -484,9 +496,11 @@ static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   const dim3 grid(a.splits, a.hk, rows);
   if (a.fp8) return launch_decode_fp8(a, rows, stream);
-  const bool up = a.page_shift >= 2;
-#define OMNI_DECODE(K, ...) \
-  (up ? K<__VA_ARGS__, true><<<grid, kDecodeThreads, 0, stream>>>(a) : K<__VA_ARGS__, false><<<grid, kDecodeThreads, 0, stream>>>(a))
+  const int slots = a.len_mode == 2 ? kSlotsDense : a.page_shift >= 2 ? kSlotsUniform : kSlotsLane;
+#define OMNI_DECODE(K, G)                                                                  \
+  (slots == kSlotsDense     ? K<G, kSlotsDense><<<grid, kDecodeThreads, 0, stream>>>(a)    \
+   : slots == kSlotsUniform ? K<G, kSlotsUniform><<<grid, kDecodeThreads, 0, stream>>>(a)  \
+                            : K<G, kSlotsLane><<<grid, kDecodeThreads, 0, stream>>>(a))
   switch (a.hq / a.hk) {
     case 1: OMNI_DECODE(decode_split, 1); break;
     case 2: OMNI_DECODE(decode_split, 2); break;

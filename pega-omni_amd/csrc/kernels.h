@@ -36,6 +36,7 @@ struct DecodeArgs {
   int fp8;           // 1: kv slots are FP8 E4M3 with f32 scales (lm_attend's cache)
   int64_t slot_bytes;  // bytes per FP8 slot: 2 hk 128 + 2 hk 4
   int group_heads;     // FP8: heads per workgroup (0 = pick from the shape)
+  int dense_per, dense_base, dense_span;  // dense rows (len_mode 2): slot (n / per) * span + t
 };
 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream);
@@ -90,6 +91,21 @@ struct RopeArgs {
   int mrope_hw;
   float eps, theta, coef;
 };
+// Head-64 ring attentions (Mimi, Qwen3-TTS codec, depformer).
+struct ShortArgs {
+  const bf16_t* qkv;
+  const int32_t* pos;
+  const int32_t* lines;  // session -> line of the per-session state
+  void* state;           // Mimi / codec rings: state + lines[s] * stride bytes
+  int64_t stride;
+  bf16_t* ws;            // depformer workspace [seqs][8][K | V][heads * 64]
+  bf16_t* out;
+  int rows, heads, T, context, step;
+  float scale, theta;
+};
+constexpr int kShortMimi = 0, kShortCodec = 1, kShortDep = 2;
+int launch_short(const ShortArgs& a, int kind, hipStream_t stream);
+
 constexpr int kRopeQwen3 = 0, kRopeQwen3Dense = 1, kRopeHidream = 2, kRopeLm = 3;
 int launch_rope(const RopeArgs& a, int mode, hipStream_t stream);
 int launch_dit(const TiledArgs& a, int batch, hipStream_t stream);

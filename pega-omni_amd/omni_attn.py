@@ -37,6 +37,10 @@ EXPORTS = (
     "omni_attn_prefill_run",
     "omni_hidream_attend",
     "omni_hidream_attend_batched",
+    "omni_qwen3_attend_dense",
+    "omni_mimi_attend",
+    "omni_codec_attention",
+    "omni_lm_dep_kv_attend",
     "omni_qwen3_rope",
     "omni_qwen3_rope_dense",
     "omni_lm_rope",
@@ -108,6 +112,10 @@ def load(path: str = LIB_PATH):
         "omni_attn_prefill_run": [pplan, P, P, P, P, P, P, P, f32, P, P],
         "omni_hidream_attend": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, P],
         "omni_hidream_attend_batched": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, i32, i64, i64, i64, P],
+        "omni_qwen3_attend_dense": [P, P, i32, i32, i32, P, i32, i32, f32, dplan, P, P],
+        "omni_mimi_attend": [P, P, P, P, P, i32, i32, i32, f32, i32, i64, P],
+        "omni_codec_attention": [P, P, P, P, P, i32, i64, i32, f32, P],
+        "omni_lm_dep_kv_attend": [P, P, i32, P, i32, i32, f32, P],
         "omni_qwen3_rope": [P, P, P, P, P, P, i32, i32, i32, f32, f32, P],
         "omni_qwen3_rope_dense": [P, P, P, P, i32, i32, i32, i32, i32, i32, f32, f32, P],
         "omni_lm_rope": [P, P, P, P, i32, i32, f32, P],
@@ -341,3 +349,38 @@ def hidream_qk_rope(qkv, ld, q_norm, k_norm, positions, slots, k_cache, v_cache,
     _check(load().omni_hidream_qk_rope(_ptr(qkv), ld, _ptr(q_norm), _ptr(k_norm), _ptr(positions), _ptr(slots),
                                        _ptr(k_cache), _ptr(v_cache), rows, hq, hk, mrope_hw, float(eps),
                                        float(theta), _stream(stream)))
+
+
+# ------------------------------------------------- dense and head-64 attentions
+def qwen3_attend_dense(qkv, kv, per, base, span, out, hq, hk, scale, plan, workspace=None, stream=None):
+    """``qwen3_attend_dense`` (crates/omni-qwen3/kernels/qwen3.cu:243-248); the
+    plan is made with page = 1 and max_len >= base + per."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
+    _check(load().omni_qwen3_attend_dense(_ptr(qkv), _ptr(kv), per, base, span, _ptr(out), hq, hk, float(scale),
+                                          ctypes.byref(plan), _ptr(workspace), _stream(stream)))
+    return out
+
+
+def mimi_attend(qkv, pos, lines, state, out, rows, T, heads, scale, context, stride, stream=None):
+    """``mimi_attend`` (crates/omni-personaplex/kernels/mimi.cu:248-263); state is
+    any contiguous device tensor holding the per-session rings."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(out, "out"), _i32_dev(pos, "pos"), _i32_dev(lines, "lines")
+    _check(load().omni_mimi_attend(_ptr(qkv), _ptr(pos), _ptr(lines), _ptr(state), _ptr(out), rows, T, heads,
+                                   float(scale), context, int(stride), _stream(stream)))
+    return out
+
+
+def codec_attention(qkv, pos, lines, kv, out, rows, stride, heads, theta, stream=None):
+    """``codec_attention`` (crates/omni-qwen3-tts/kernels/codec.cu:168-277)."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(out, "out"), _i32_dev(pos, "pos"), _i32_dev(lines, "lines")
+    _check(load().omni_codec_attention(_ptr(qkv), _ptr(pos), _ptr(lines), _ptr(kv), _ptr(out), rows, int(stride),
+                                       heads, float(theta), _stream(stream)))
+    return out
+
+
+def lm_dep_kv_attend(qkv, ws, step, out, rows, heads, scale, stream=None):
+    """``lm_dep_kv_attend`` (crates/omni-personaplex/kernels/lm.cu:314-366)."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(ws, "ws"), _bf16_dev(out, "out")
+    _check(load().omni_lm_dep_kv_attend(_ptr(qkv), _ptr(ws), step, _ptr(out), rows, heads, float(scale),
+                                        _stream(stream)))
+    return out

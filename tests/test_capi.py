@@ -159,3 +159,17 @@ def test_rope_entry_points_validate_before_launch():
     assert L.omni_hidream_qk_rope(f, 128, f, f, f, f, f, f, 4, 4, 2, 20, 1e-6, 1e6, None) == oa.EINVAL  # ld too short
     assert L.omni_hidream_qk_rope(f, 1024, f, f, f, f, f, f, 4, 4, 2, 22, 1e-6, 1e6, None) == oa.EINVAL
     assert "mrope_hw" in L.omni_attn_last_error().decode()
+
+
+def test_short_entry_points_validate_before_launch():
+    L = oa.load()
+    f = ctypes.c_void_p(4096)
+    p = oa.decode_plan(4, 16, 8, 1, 20)
+    assert L.omni_qwen3_attend_dense(f, f, 5, 7, 10, f, 16, 8, 0.1, ctypes.byref(p), f, None) == oa.EINVAL
+    small = oa.decode_plan(4, 16, 8, 1, 8)
+    assert L.omni_qwen3_attend_dense(f, f, 5, 7, 16, f, 16, 8, 0.1, ctypes.byref(small), f, None) == oa.EINVAL
+    assert L.omni_mimi_attend(f, f, f, f, f, 4, 0, 8, 0.125, 250, 1024, None) == oa.EINVAL
+    assert L.omni_mimi_attend(f, f, f, f, f, 4, 2, 8, 0.125, 250, 1000, None) == oa.EINVAL  # stride not 16-aligned
+    assert L.omni_codec_attention(f, f, f, f, f, 4, 1024, 8, -1.0, None) == oa.EINVAL
+    assert L.omni_lm_dep_kv_attend(f, f, 8, f, 4, 16, 0.125, None) == oa.EINVAL
+    assert L.omni_lm_dep_kv_attend(f, f, 0, f, 0, 16, 0.125, None) == oa.OK
