@@ -318,6 +318,74 @@ def rope_bench(stream, steps, warmup):
     return res
 
 
+def short_bench(stream, steps, warmup):
+    """The small attentions at engine shapes, one launch per step: the code
+    predictor's qwen3_attend_dense (64 sessions at position 15 of a 16-slot
+    workspace), Mimi's ring attention (128 sessions x 2 rows, 8 heads, full
+    250-slot rings), the codec decoder's fused attention (64 sessions, 16
+    heads, a full 72-frame ring) and the depformer's last step (128 sessions,
+    16 heads, step 7). Bytes: K/V rows read once per (row, head), q, out, writes."""
+    import numpy as np
+    import torch
+
+    import omni_attn as oa
+
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+    bf = lambda *shape: torch.randn(*shape, device="cuda", generator=gen).to(torch.bfloat16)
+    res = {}
+
+    def run(name, call, bytes_):
+        def step(s, ev):
+            if ev is not None:
+                ev[0][0].record(s)
+            call(s)
+            if ev is not None:
+                ev[0][1].record(s)
+
+        ms, launch_ms = time_steps(step, steps * 5, warmup, stream, per_launch=1)
+        res[name] = dict(bytes=bytes_, launch_us=round(launch_ms * 1e3, 2),
+                         gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1))
+
+    # code predictor: hq16/hk8, one row per session at position 15
+    rows, hq, hk = 64, 16, 8
+    qkv, kv = bf(rows, (hq + 2 * hk) * 128), bf(rows * 16, 2 * hk * 128)
+    out = torch.empty(rows, hq * 128, dtype=torch.bfloat16, device="cuda")
+    plan = oa.decode_plan(rows, hq, hk, 1, 16)
+    ws = oa.workspace_for(plan)
+    run("qwen3_attend_dense code predictor", lambda s: oa.qwen3_attend_dense(qkv, kv, 1, 15, 16, out, hq, hk, 0.088,
+                                                                             plan, ws, s),
+        rows * 16 * hk * 512 + rows * hq * 512)
+    # Mimi: 8 heads of 64, T = 2, context 250, full rings
+    sess, T, heads, ctx = 128, 2, 8, 250
+    stride = ctx * 2 * heads * 64 * 2
+    state = torch.empty(sess * stride, dtype=torch.uint8, device="cuda")
+    state.view(torch.bfloat16).copy_(bf(sess * stride // 2))
+    qkv, out = bf(sess * T, 3 * heads * 64), torch.empty(sess * T, heads * 64, dtype=torch.bfloat16, device="cuda")
+    pos, lines = i32(np.full(sess, 500)), i32(np.arange(sess))
+    run("mimi_attend", lambda s: oa.mimi_attend(qkv, pos, lines, state, out, sess * T, T, heads, 0.125, ctx, stride,
+                                                s),
+        sess * T * heads * (ctx * 256 + 256))
+    # codec decoder: 16 heads of 64, full 72-frame rings
+    sess, heads = 64, 16
+    width = heads * 64
+    stride = 2 * 72 * width * 2
+    ring = torch.empty(sess * stride, dtype=torch.uint8, device="cuda")
+    ring.view(torch.bfloat16).copy_(bf(sess * stride // 2))
+    qkv, out = bf(sess, 3 * width), torch.empty(sess, width, dtype=torch.bfloat16, device="cuda")
+    pos = i32(np.full(sess, 1000))
+    run("codec_attention", lambda s: oa.codec_attention(qkv, pos, lines[:sess], ring, out, sess, stride, heads, 1e4, s),
+        sess * heads * (72 * 256 + 3 * 128 + 128))
+    # depformer: 16 heads of 64, step 7
+    sess, heads = 128, 16
+    width = heads * 64
+    qkv, wsd = bf(sess, 3 * width), bf(sess, 8 * 2 * width)
+    out = torch.empty(sess, width, dtype=torch.bfloat16, device="cuda")
+    run("lm_dep_kv_attend step 7", lambda s: oa.lm_dep_kv_attend(qkv, wsd, 7, out, sess, heads, 0.125, s),
+        sess * heads * (8 * 256 + 4 * 128))
+    return res
+
+
 def measure_peaks(stream):
     """Measured ceilings on this GPU (libomni_peaks.so): bf16 MFMA TFLOP/s
     (4 independent 32x32x16 chains per wave), v_exp_f32 and v_fma_f32 lane
@@ -390,7 +458,7 @@ def main():
     ap.add_argument("--pools", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter)")
+    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
     args = ap.parse_args()
@@ -453,7 +521,12 @@ def main():
         extra["rope"] = rope_bench(stream, args.steps, args.warmup)
         log(f"[bench] {extra['rope']}")
         torch.cuda.empty_cache()
-    if args.only in (4, 5, 2, 6, 7):
+    if args.only in (0, 8):
+        log("[bench] dense and head-64 attentions")
+        extra["short"] = short_bench(stream, args.steps, args.warmup)
+        log(f"[bench] {extra['short']}")
+        torch.cuda.empty_cache()
+    if args.only in (4, 5, 2, 6, 7, 8):
         print(json.dumps({"extra": extra}), flush=True)
         return
 

@@ -179,14 +179,19 @@ __global__ __launch_bounds__(64) void codec_attention64(ShortArgs a) {
   widen8(ldg16(row + 8 * c), qk[0]);
   widen8(ldg16(row + width + 8 * c), qk[1]);
   const uint4 cur_v = ldg16(row + 2 * width + 8 * c);
+  // The 32 angles once, one pair per lane, through LDS.
+  __shared__ float s_cos[kD / 2], s_sin[kD / 2];
+  if (lane < kD / 2) {
+    const float inv_freq = 1.f / powf(a.theta, (float)(2 * lane) / kD);
+    sincosf((float)p * inv_freq, &s_sin[lane], &s_cos[lane]);
+  }
+  __syncthreads();
   const bool lo = c < 4;
   float rot[2][8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int i = 8 * (c & 3) + e;
-    const float inv_freq = 1.f / powf(a.theta, (float)(2 * i) / kD);
-    float sn, cs;
-    sincosf((float)p * inv_freq, &sn, &cs);
+    const float cs = s_cos[i], sn = s_sin[i];
 #pragma unroll
     for (int w = 0; w < 2; ++w) {
       const float partner = xor_lane(qk[w][e], 4);
