@@ -213,15 +213,17 @@ def prefill_bench(stream, steps, warmup):
         if ev is not None:
             ev[0][1].record(s)
 
-    ms, launch_ms = time_steps(step, steps, warmup, stream, per_launch=1)
+    # MFMA legs warm for at least 20 calls: the clock ramps over the first ~100 ms of MFMA load.
+    ms, launch_ms = time_steps(step, steps, max(warmup, 20), stream, per_launch=1)
     fl = W.prefill_flops(c)
     return dict(workload="config4: " + W.CONFIGS[4]["desc"], rows=c.rows, flops=fl, ms_per_step=round(ms, 4),
                 tflops=round(fl / (ms * 1e-3) / 1e12, 2), launch_us=round(launch_ms * 1e3, 2),
                 frac=round(fl / (launch_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
 
-def dit_bench(stream, steps, warmup, hk=8):
-    """Config 5: the HiDream CFG pair's full attention, one launch per step."""
+def dit_bench(stream, steps, warmup, hk=8, split=True):
+    """Config 5: the HiDream CFG pair's full attention, one call per step
+    (the tiled kernel, plus the tail-split combine when `split`)."""
     import numpy as np
     import torch
 
@@ -242,17 +244,19 @@ def dit_bench(stream, steps, warmup, hk=8):
     out = torch.empty(c.batch, c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
     kvl = torch.tensor([c.kv_len], dtype=torch.int32, device="cuda")
 
+    ws = oa.hidream_workspace() if split else None
+
     def step(s, ev):
         if ev is not None:
             ev[0][0].record(s)
-        oa.hidream_attend_batched(q, k, v, out, c.q_len, kvl, c.q_stride, 0, c.scale_log2, c.hq, hk, c.batch,
-                                  c.q_len * c.q_stride, c.kv_len * hk * 128, c.q_len * c.hq * 128, s)
+        oa.hidream_attend_ws(q, k, v, out, c.q_len, kvl, c.q_stride, 0, c.scale_log2, c.hq, hk, c.batch,
+                             c.q_len * c.q_stride, c.kv_len * hk * 128, c.q_len * c.hq * 128, ws, s)
         if ev is not None:
             ev[0][1].record(s)
 
-    ms, launch_ms = time_steps(step, steps, warmup, stream, per_launch=1)
+    ms, launch_ms = time_steps(step, steps, max(warmup, 20), stream, per_launch=1)
     fl = c.flops()
-    return dict(workload=f"config5: {W.CONFIGS[5]['desc']} (hk={hk})", flops=fl, ms_per_step=round(ms, 4),
+    return dict(workload=f"config5: {W.CONFIGS[5]['desc']} (hk={hk})", split=split, flops=fl, ms_per_step=round(ms, 4),
                 tflops=round(fl / (ms * 1e-3) / 1e12, 2), launch_us=round(launch_ms * 1e3, 2),
                 frac=round(fl / (launch_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
@@ -492,6 +496,10 @@ def main():
         log(f"[bench] {extra['config5']}")
         if args.only == 0:
             extra["config5_mha"] = dit_bench(stream, args.steps, args.warmup, hk=32)
+        if args.only == 5:  # A/B of the tail split, alternating
+            for i in range(2):
+                extra[f"config5_unsplit_{i}"] = dit_bench(stream, args.steps, args.warmup, split=False)
+                extra[f"config5_split_{i}"] = dit_bench(stream, args.steps, args.warmup)
     if args.only in (0, 2):
         log("[bench] config 2 decode")
         b2 = DecodeBench(2, args.pools, chunk=args.chunk)

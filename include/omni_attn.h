@@ -229,6 +229,20 @@ int omni_hidream_qk_rope(void* qkv, int ld, const void* q_norm, const void* k_no
                          const int32_t* slots, void* k_cache, void* v_cache, int rows, int hq, int hk, int mrope_hw,
                          float eps, float theta, void* stream);
 
+/* The batched call with a workspace: the last fraction of a round of tiles
+ * (tiles % resident workgroups) is split by keys into chunks that fill the
+ * round, and a combine kernel merges the chunks (log-sum-exp). Same results
+ * to rounding; workspace NULL runs unsplit. workspace_bytes must be at least
+ * omni_hidream_workspace_bytes() (16-byte aligned); the split depends only on
+ * the shape and the device, never on *kv_len_at. */
+int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
+                           int q_stride, int causal, float scale_log2, int hq, int hk, int batch, int64_t q_bstride,
+                           int64_t kv_bstride, int64_t out_bstride, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/* Workspace bytes omni_hidream_attend_ws needs at most on the current device. */
+int64_t omni_hidream_workspace_bytes(void);
+
 /* ------------------------------------------------------------- library */
 
 /* Library version (major * 10000 + minor * 100 + patch). */

@@ -334,6 +334,69 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
   return ok();
 }
 
+namespace {
+
+// Workgroups of the tiled kernel resident at once on the current device (two per CU).
+int resident_tiled_groups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return 2 * cus;
+}
+
+}  // namespace
+
+int64_t omni_hidream_workspace_bytes(void) { return (int64_t)resident_tiled_groups() * omni::kSegmentBytes; }
+
+int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
+                           int q_stride, int causal, float scale_log2, int hq, int hk, int batch, int64_t q_bstride,
+                           int64_t kv_bstride, int64_t out_bstride, void* workspace, int64_t workspace_bytes,
+                           void* stream) {
+  if (!workspace)
+    return omni_hidream_attend_batched(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, batch,
+                                       q_bstride, kv_bstride, out_bstride, stream);
+  if (q_len < 0 || batch < 0) return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_len=%d batch=%d", q_len, batch);
+  if (q_len == 0 || batch == 0) return ok();
+  if (!q || !k || !v || !out || !kv_len_at) return fail(OMNI_ATTN_EINVAL, "hidream_attend: null device pointer");
+  if (hk <= 0 || hq <= 0 || hq % hk != 0)
+    return fail(OMNI_ATTN_EINVAL, "hidream_attend: hq=%d is not a multiple of hk=%d", hq, hk);
+  const int G = hq / hk;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: hq/hk=%d not in {1,2,4,8}", G);
+  if (q_stride < hq * OMNI_ATTN_HEAD_DIM || q_stride % 8 != 0)
+    return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_stride=%d", q_stride);
+  if (batch > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: batch=%d", batch);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
+    return fail(OMNI_ATTN_EINVAL, "hidream_attend: workspace must be 16-byte aligned");
+  omni::TiledArgs a{};
+  a.q = static_cast<const omni::bf16_t*>(q);
+  a.q_stride = q_stride;
+  a.k = static_cast<const omni::bf16_t*>(k);
+  a.v = static_cast<const omni::bf16_t*>(v);
+  a.kv_len_at = kv_len_at;
+  a.q_len = q_len;
+  a.causal = causal ? 1 : 0;
+  a.q_bstride = q_bstride;
+  a.kv_bstride = kv_bstride;
+  a.out_bstride = out_bstride;
+  a.out = static_cast<omni::bf16_t*>(out);
+  a.hq = hq;
+  a.hk = hk;
+  a.scale_log2 = scale_log2;
+  int items = 0;
+  omni::dit_split(a, batch, resident_tiled_groups(), &items, &a.split_from, &a.split_k);
+  const int64_t need = (int64_t)(items - a.split_from) * a.split_k * omni::kSegmentBytes;
+  if (need > workspace_bytes)
+    return fail(OMNI_ATTN_EWORKSPACE, "hidream_attend: the split needs %lld workspace bytes, got %lld",
+                (long long)need, (long long)workspace_bytes);
+  a.ws = static_cast<float*>(workspace);
+  const int rc = omni::launch_dit(a, batch, as_stream(stream));
+  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: shape not implemented");
+  if (rc != 0)
+    return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed: %s", hipGetErrorString(omni::g_launch_status));
+  return ok();
+}
+
 int omni_hidream_attend(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
                         int q_stride, int causal, float scale_log2, int hq, int hk, void* stream) {
   return omni_hidream_attend_batched(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, 1, 0, 0, 0,

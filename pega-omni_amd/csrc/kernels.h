@@ -67,9 +67,16 @@ struct TiledArgs {
   bf16_t* out;
   int hq, hk;
   float scale_log2;
+  // Tail split (dense, uniform key ranges): items >= split_from run as
+  // split_k key chunks each, writing f32 partials to ws (one segment per
+  // chunk: O[128 rows][128] then (m, l)[128 rows]); 0 chunks = no split.
+  int split_from, split_k;
+  float* ws;
 };
 
-constexpr int kTiledRows = 128;  // packed (position, head) query rows per MFMA tile
+constexpr int kTiledRows = 128;
+// Bytes of one partial segment of the tail split: O (f32) and (m, l) per packed row.
+constexpr int64_t kSegmentBytes = (int64_t)kTiledRows * (128 + 2) * 4;  // packed (position, head) query rows per MFMA tile
 
 int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream);
 
@@ -109,5 +116,7 @@ int launch_short(const ShortArgs& a, int kind, hipStream_t stream);
 constexpr int kRopeQwen3 = 0, kRopeQwen3Dense = 1, kRopeHidream = 2, kRopeLm = 3;
 int launch_rope(const RopeArgs& a, int mode, hipStream_t stream);
 int launch_dit(const TiledArgs& a, int batch, hipStream_t stream);
+// Items and the tail split launch_dit would use for a call (split_k = 0: none).
+void dit_split(const TiledArgs& a, int batch, int resident, int* items, int* split_from, int* split_k);
 
 }  // namespace omni

@@ -93,9 +93,30 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   // batch) share that XCD's L2.
   // Prefill: the work list is longest-first, so items go out in order with
   // the kv heads of one tile side by side (spread over the XCDs).
-  const int per = (items + 7) >> 3;
-  const int idx = PAGED ? (int)blockIdx.x : (int)((blockIdx.x & 7) * per + (blockIdx.x >> 3));
-  if (idx >= items) return;
+  // DiT tail split: the first split_from items run whole, then every later
+  // item runs as split_k key chunks (workgroups dispatched after all whole
+  // items, so they fill the last round), each with its own XCD-aware order.
+  int idx, chunk = -1;
+  if (!PAGED && a.split_k > 0) {
+    const int whole8 = ((a.split_from + 7) >> 3) << 3;
+    if ((int)blockIdx.x < whole8) {
+      const int per = whole8 >> 3;
+      idx = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+      if (idx >= a.split_from) return;
+    } else {
+      const int b2 = blockIdx.x - whole8;
+      const int units = (items - a.split_from) * a.split_k;
+      const int per = (units + 7) >> 3;
+      const int u = (b2 & 7) * per + (b2 >> 3);
+      if (u >= units) return;
+      idx = a.split_from + u / a.split_k;
+      chunk = u % a.split_k;
+    }
+  } else {
+    const int per = (items + 7) >> 3;
+    idx = PAGED ? (int)blockIdx.x : (int)((blockIdx.x & 7) * per + (blockIdx.x >> 3));
+    if (idx >= items) return;
+  }
   const int tile = PAGED ? idx / a.hk : idx % ntiles;
   const int kvh = PAGED ? idx % a.hk : (idx / ntiles) % a.hk;
   const int b = PAGED ? 0 : idx / (ntiles * a.hk);
@@ -209,14 +230,17 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   const int vg = lane >> 4, vi = lane & 15;
   const int v_lane = (4 * (vg >> 1) + (vi >> 2)) * kHead + 32 * (vi >> 2) + 16 * (vg & 1) + 4 * (vi & 3);
 
+  // Key tiles [s_lo, s_hi): all of them, or this chunk's share.
   const int steps = (t.last + kBN - 1) / kBN;
-  if (steps > 0) issue_tile(0, smem0);
+  const int s_lo = chunk < 0 ? 0 : chunk * steps / a.split_k;
+  const int s_hi = chunk < 0 ? steps : (chunk + 1) * steps / a.split_k;
+  if (s_hi > s_lo) issue_tile(s_lo * kBN, smem0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first tile is in LDS
   __syncthreads();
   // One key tile: start loading the next tile into `nxt`, compute from `cur`.
   auto tile_step = [&](int st, const bf16_t* cur, bf16_t* nxt) {
     const int n0 = st * kBN;
-    if (st + 1 < steps) issue_tile(n0 + kBN, nxt);  // lands while this tile computes
+    if (st + 1 < s_hi) issue_tile(n0 + kBN, nxt);  // lands while this tile computes
     const bf16_t* kt = cur;
     const bf16_t* vt = cur + kTileElems;  // V tile
 
@@ -297,13 +321,25 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
     __syncthreads();
   };
-  for (int st = 0; st < steps; st += 2) {
+  for (int st = s_lo; st < s_hi; st += 2) {
     tile_step(st, smem0, smem1);
-    if (st + 1 < steps) tile_step(st + 1, smem1, smem0);
+    if (st + 1 < s_hi) tile_step(st + 1, smem1, smem0);
   }
 
-  // Normalise and store: register e of block md is dim 32 md + 8 (e / 4) + 4 h + e % 4.
+  // Register e of block md is dim 32 md + 8 (e / 4) + 4 h + e % 4.
   l += xor_lane(l, 32);
+  if (chunk >= 0) {  // a chunk's partial: unnormalised O with its base m and sum l, for dit_combine
+    float* seg = a.ws + (int64_t)((idx - a.split_from) * a.split_k + chunk) * (kBM * (kHead + 2));
+#pragma unroll
+    for (int md = 0; md < 4; ++md)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(seg + r * kHead + 32 * md + 8 * q4 + 4 * h) =
+            make_float4(o[md][4 * q4], o[md][4 * q4 + 1], o[md][4 * q4 + 2], o[md][4 * q4 + 3]);
+    if (h == 0) *reinterpret_cast<float2*>(seg + kBM * kHead + 2 * r) = make_float2(m, l);
+    return;
+  }
+  // Normalise and store.
   if (!row_ok) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
   bf16_t* dst = t.out + ((int64_t)p * a.hq + head) * kHead;
@@ -319,10 +355,56 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     }
 }
 
+// Merge the split_k chunk partials of each split DiT item into its output
+// rows: one workgroup per (item, 16 packed rows), 16 threads per row, 8 dims
+// each (two 16-byte partial loads per chunk).
+constexpr int kCombineRows = 16;
+
+__global__ __launch_bounds__(256) void dit_combine(TiledArgs a, int ntiles) {
+  const int idx = a.split_from + blockIdx.x;
+  const int G = a.hq / a.hk, kpos = kBM / G;
+  const int tile = idx % ntiles, kvh = (idx / ntiles) % a.hk, b = idx / (ntiles * a.hk);
+  const int q0 = tile * kpos, nq = min(kpos, a.q_len - q0);
+  const int r = blockIdx.y * kCombineRows + (threadIdx.x >> 4), d0 = 8 * (threadIdx.x & 15);
+  const int p = r / G, head = kvh * G + r % G;
+  if (p >= nq) return;
+  constexpr int kSeg = kBM * (kHead + 2);
+  const float* seg0 = a.ws + (int64_t)(blockIdx.x * a.split_k) * kSeg;
+  float top = -INFINITY;
+  for (int c = 0; c < a.split_k; ++c) top = fmaxf(top, seg0[c * kSeg + kBM * kHead + 2 * r]);
+  float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  for (int c = 0; c < a.split_k; ++c) {
+    const float* seg = seg0 + c * kSeg;
+    const float2 ml = *reinterpret_cast<const float2*>(seg + kBM * kHead + 2 * r);
+    const float w = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - top);
+    den = fmaf(ml.y, w, den);
+    const float4 v0 = *reinterpret_cast<const float4*>(seg + r * kHead + d0);
+    const float4 v1 = *reinterpret_cast<const float4*>(seg + r * kHead + d0 + 4);
+    num[0] = fmaf(v0.x, w, num[0]);
+    num[1] = fmaf(v0.y, w, num[1]);
+    num[2] = fmaf(v0.z, w, num[2]);
+    num[3] = fmaf(v0.w, w, num[3]);
+    num[4] = fmaf(v1.x, w, num[4]);
+    num[5] = fmaf(v1.y, w, num[5]);
+    num[6] = fmaf(v1.z, w, num[6]);
+    num[7] = fmaf(v1.w, w, num[7]);
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  uint4 o;
+  o.x = pack_bf16x2(num[0] * inv, num[1] * inv);
+  o.y = pack_bf16x2(num[2] * inv, num[3] * inv);
+  o.z = pack_bf16x2(num[4] * inv, num[5] * inv);
+  o.w = pack_bf16x2(num[6] * inv, num[7] * inv);
+  *reinterpret_cast<uint4*>(a.out + b * a.out_bstride + ((int64_t)(q0 + p) * a.hq + head) * kHead + d0) = o;
+}
+
 template <bool PAGED>
 int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) {
   if (items <= 0) return 0;
-  const int grid = ((items + 7) >> 3) << 3;
+  int grid = ((items + 7) >> 3) << 3;
+  if (!PAGED && a.split_k > 0)
+    grid = (((a.split_from + 7) >> 3) << 3) + ((((items - a.split_from) * a.split_k + 7) >> 3) << 3);
   switch (a.hq / a.hk) {
 #define OMNI_CASE(G)                                                                       \
   case G:                                                                                  \
@@ -335,7 +417,12 @@ int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) 
 #undef OMNI_CASE
     default: return -2;
   }
-  return check_launch();
+  if (check_launch() != 0) return -3;
+  if (!PAGED && a.split_k > 0) {
+    dit_combine<<<dim3(items - a.split_from, kBM / kCombineRows), 256, 0, stream>>>(a, ntiles);
+    return check_launch();
+  }
+  return 0;
 }
 
 int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream) {
@@ -349,6 +436,23 @@ int launch_dit(const TiledArgs& a, int batch, hipStream_t stream) {
   const long long items = (long long)ntiles * a.hk * batch;
   if (items > (1LL << 30)) return -2;
   return launch_tiled<false>(a, (int)items, ntiles, stream);
+}
+
+// With `resident` workgroups in flight (two per CU), items - items % resident
+// run whole and the rest each split into resident / (items % resident) key
+// chunks, so the last round is full instead of a fraction.
+void dit_split(const TiledArgs& a, int batch, int resident, int* items, int* split_from, int* split_k) {
+  const int G = a.hq / a.hk;
+  const int ntiles = (a.q_len + kBM / G - 1) / (kBM / G);
+  const long long n = (long long)ntiles * a.hk * batch;
+  *items = (int)n;
+  *split_from = (int)n;
+  *split_k = 0;
+  if (resident <= 0 || n <= 0 || n > (1LL << 30)) return;
+  const int rem = (int)(n % resident);
+  if (rem == 0 || resident / rem < 2) return;
+  *split_from = (int)n - rem;
+  *split_k = resident / rem;
 }
 
 }  // namespace omni

@@ -37,6 +37,8 @@ EXPORTS = (
     "omni_attn_prefill_run",
     "omni_hidream_attend",
     "omni_hidream_attend_batched",
+    "omni_hidream_attend_ws",
+    "omni_hidream_workspace_bytes",
     "omni_qwen3_attend_dense",
     "omni_mimi_attend",
     "omni_codec_attention",
@@ -112,6 +114,8 @@ def load(path: str = LIB_PATH):
         "omni_attn_prefill_run": [pplan, P, P, P, P, P, P, P, f32, P, P],
         "omni_hidream_attend": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, P],
         "omni_hidream_attend_batched": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, i32, i64, i64, i64, P],
+        "omni_hidream_attend_ws": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, i32, i64, i64, i64, P, i64, P],
+        "omni_hidream_workspace_bytes": [],
         "omni_qwen3_attend_dense": [P, P, i32, i32, i32, P, i32, i32, f32, dplan, P, P],
         "omni_mimi_attend": [P, P, P, P, P, i32, i32, i32, f32, i32, i64, P],
         "omni_codec_attention": [P, P, P, P, P, i32, i64, i32, f32, P],
@@ -126,7 +130,8 @@ def load(path: str = LIB_PATH):
     for name, args in sig.items():
         fn = getattr(L, name)
         fn.argtypes = args
-        fn.restype = ctypes.c_char_p if name == "omni_attn_last_error" else ctypes.c_int
+        fn.restype = (ctypes.c_char_p if name == "omni_attn_last_error"
+                      else ctypes.c_int64 if name == "omni_hidream_workspace_bytes" else ctypes.c_int)
     _lib = L
     return L
 
@@ -383,4 +388,22 @@ def lm_dep_kv_attend(qkv, ws, step, out, rows, heads, scale, stream=None):
     _bf16_dev(qkv, "qkv"), _bf16_dev(ws, "ws"), _bf16_dev(out, "out")
     _check(load().omni_lm_dep_kv_attend(_ptr(qkv), _ptr(ws), step, _ptr(out), rows, heads, float(scale),
                                         _stream(stream)))
+    return out
+
+
+def hidream_workspace(device="cuda"):
+    """A workspace for hidream_attend_ws on the current device."""
+    import torch
+
+    return torch.empty(int(load().omni_hidream_workspace_bytes()), dtype=torch.uint8, device=device)
+
+
+def hidream_attend_ws(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, batch, q_bstride,
+                      kv_bstride, out_bstride, workspace, stream=None):
+    """The batched DiT call with the tail split (a workspace from hidream_workspace)."""
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _check(load().omni_hidream_attend_ws(_ptr(q), _ptr(k), _ptr(v), _ptr(out), q_len, _ptr(kv_len_at), q_stride,
+                                         int(causal), float(scale_log2), hq, hk, batch, int(q_bstride),
+                                         int(kv_bstride), int(out_bstride), _ptr(workspace), nbytes,
+                                         _stream(stream)))
     return out

@@ -106,3 +106,44 @@ def test_dit_config5_subset(oracle):
     sub = W.DenseCase(hq=32, hk=8, q_len=256, kv_len=4352, causal=0, q_stride=c.q_stride, q=c.q, k=c.k, v=c.v)
     want = oracle_dense(oracle, sub)
     assert_close(got[:256], want, what="config5 first 256 rows")
+
+
+def run_dense_ws(c, kv_len=None):
+    q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
+    out = torch.zeros(c.batch, c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    kvl = dev_i32(np.array([kv_len or c.kv_len], np.int32))
+    ws = oa.hidream_workspace()
+    ws.fill_(0xFF)  # stale partials must not matter
+    oa.hidream_attend_ws(q, k, v, out, c.q_len, kvl, c.q_stride, c.causal, c.scale_log2, c.hq, c.hk, c.batch,
+                         c.q_len * c.q_stride, c.kv_len * c.hk * 128, c.q_len * c.hq * 128, ws)
+    torch.cuda.synchronize()
+    return host_bits(out)
+
+
+@pytest.mark.parametrize("hq,hk,q_len,kv_len,causal,batch", [
+    (8, 2, 256, 256, 0, 1),     # 16 tiles: every tile split into 32 chunks of a 4-tile key range (most empty)
+    (32, 8, 300, 700, 1, 2),    # causal: chunk ranges differ per tile
+    (32, 8, 1000, 1000, 0, 1),  # 256 tiles: every tile split in two
+    (4, 4, 1, 1, 0, 1),
+])
+def test_dit_tail_split_parity(oracle, hq, hk, q_len, kv_len, causal, batch):
+    c = W.dense_case(hq, hk, q_len, kv_len, causal, batch=batch, seed=q_len + kv_len)
+    got = run_dense_ws(c)
+    for b in range(batch):
+        assert_close(got[b], oracle_dense(oracle, c, b), what=f"ws dit {hq}/{hk} {q_len}x{kv_len} c{causal} b{b}")
+
+
+def test_dit_tail_split_config5_matches_unsplit(oracle):
+    """Config 5 (2176 tiles: 2048 whole, 128 split into 4 chunks on a 256-CU
+    GPU) agrees with the unsplit kernel everywhere and with the oracle on the
+    last 128 query positions (all in split tiles)."""
+    c = W.dense_case(32, 8, 4352, 4352, 0, batch=2, seed=5000)
+    got, ref = run_dense_ws(c), run_dense(c)
+    for b in range(2):
+        assert_close(got[b], ref[b], what=f"ws vs unsplit batch {b}")
+    sub = W.DenseCase(hq=32, hk=8, q_len=4352, kv_len=4352, causal=0, q_stride=c.q_stride, q=c.q, k=c.k, v=c.v)
+    tail = oracle.dense_attend(np.ascontiguousarray(c.q[1, -128:]), np.ascontiguousarray(c.k[1]),
+                               np.ascontiguousarray(c.v[1]), 128, 4352, c.q_stride, 32, 8, 0, c.scale_log2,
+                               nthreads=16)
+    assert_close(got[1, -128:], tail, what="config5 split tail vs oracle")
+    del sub
