@@ -188,8 +188,36 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   // Keys past `last` repeat the last key (their scores are masked).
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   typedef __attribute__((address_space(3))) void lds_void;
+  // Dense sources: within a full tile a lane's rows and chunks are fixed, so
+  // its element offsets from the tile's first key are constants (32-bit) and a
+  // tile adds one uniform base: loads take a scalar base and a vector offset.
+  uint32_t koff[kRowsPerWave / 4], voff[kRowsPerWave / 4];
+  if constexpr (!PAGED) {
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / 4; ++i) {
+      const int row = kRowsPerWave * wave_u + 4 * i + (lane >> 4);
+      const int cs = lane & 15;
+      const int kc = cs ^ (row & 15);
+      const int vc = (((cs >> 2) ^ (row & 3)) << 2) | (cs & 3);
+      koff[i] = (uint32_t)(row * t.kv_stride + 8 * kc);
+      voff[i] = (uint32_t)(row * t.kv_stride + 8 * vc);
+    }
+  }
   auto issue_tile = [&](int n0, bf16_t* kd) {
     bf16_t* vd = kd + kTileElems;
+    if constexpr (!PAGED) {
+      if (n0 + kBN <= t.last) {  // a full tile: no clamping
+        const bf16_t* kb = t.kbase + (int64_t)n0 * t.kv_stride;
+        const bf16_t* vb = t.vbase + (int64_t)n0 * t.kv_stride;
+#pragma unroll
+        for (int i = 0; i < kRowsPerWave / 4; ++i) {
+          const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;
+          __builtin_amdgcn_global_load_lds(kb + koff[i], (lds_void*)(kd + lrow), 16, 0, 0);
+          __builtin_amdgcn_global_load_lds(vb + voff[i], (lds_void*)(vd + lrow), 16, 0, 0);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
       const int row = kRowsPerWave * wave_u + 4 * i + (lane >> 4);

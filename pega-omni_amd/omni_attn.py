@@ -87,11 +87,13 @@ class PrefillPlan(ctypes.Structure):
 _lib = None
 
 
-def load(path: str = LIB_PATH):
-    """Load the HIP library (raises if it was not built)."""
+def load(path: str | None = None):
+    """Load the HIP library (raises if it was not built). OMNI_ATTN_LIB names
+    another build of the same library (A/B measurements)."""
     global _lib
     if _lib is not None:
         return _lib
+    path = path or os.environ.get("OMNI_ATTN_LIB") or LIB_PATH
     if not os.path.exists(path):
         raise OmniAttnError(ELAUNCH, f"{path} is missing: build it with pega-omni_amd/build.py")
     # torch brings its own HIP runtime; load it first so the library binds to
