@@ -272,24 +272,30 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     const bf16_t* kt = cur;
     const bf16_t* vt = cur + kTileElems;  // V tile
 
-    // S^T = K . Q^T for keys n0 .. n0 + 63: all 16 K fragments first, then
-    // two interleaved MFMA chains.
-    uint4 kf[2][8];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-        kf[mb][kk] = *reinterpret_cast<const uint4*>(kt + (k_lane ^ (16 * kk)) + mb * 4096);
+    // S^T = K . Q^T for keys n0 .. n0 + 63: two interleaved MFMA chains
+    // (key blocks mb = 0, 1) over the 8 K-steps, with the K fragments read
+    // from LDS two K-steps ahead of use; the stages are pinned in this order.
     f32x16 sc[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[mb][e] = 0.f;
+    uint4 kf[8][2];
+    auto read_k = [&](int kk) {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
+      for (int mb = 0; mb < 2; ++mb) kf[kk][mb] = *reinterpret_cast<const uint4*>(kt + (k_lane ^ (16 * kk)) + mb * 4096);
+    };
+    read_k(0);
+    read_k(1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
-        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[mb][kk]), qf[kk], sc[mb], 0, 0, 0);
+        sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[kk][mb]), qf[kk], sc[mb], 0, 0, 0);
+      if (kk + 2 < 8) read_k(kk + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 
     // Register e of block mb is key n0 + 32 mb + 8 (e / 4) + 4 h + e % 4.
     if (__any(n0 + kBN > lim)) {
