@@ -191,32 +191,53 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   // Dense sources: within a full tile a lane's rows and chunks are fixed, so
   // its element offsets from the tile's first key are constants (32-bit) and a
   // tile adds one uniform base: loads take a scalar base and a vector offset.
+  // Paged sources with page >= 16: a wave's 16 rows of a tile are 16
+  // consecutive keys of one page, so a full tile needs one (scalar) page id
+  // per wave, read a tile ahead, and the rows are consecutive slots.
+  const bool page16 = PAGED && a.page_shift >= 4;
+  // Element offsets of this lane's rows from the first row of a wave's block
+  // of 16 (dense: from the tile's first key): constants within full tiles.
   uint32_t koff[kRowsPerWave / 4], voff[kRowsPerWave / 4];
-  if constexpr (!PAGED) {
+  {
+    const int64_t stride = PAGED ? t.per_slot : t.kv_stride;
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
-      const int row = kRowsPerWave * wave_u + 4 * i + (lane >> 4);
+      const int wrow = 4 * i + (lane >> 4);  // row within the wave's 16
+      const int row = kRowsPerWave * wave_u + wrow;
       const int cs = lane & 15;
       const int kc = cs ^ (row & 15);
       const int vc = (((cs >> 2) ^ (row & 3)) << 2) | (cs & 3);
-      koff[i] = (uint32_t)(row * t.kv_stride + 8 * kc);
-      voff[i] = (uint32_t)(row * t.kv_stride + 8 * vc);
+      const int64_t r0 = PAGED ? wrow : row;
+      koff[i] = (uint32_t)(r0 * stride + 8 * kc);
+      voff[i] = (uint32_t)(r0 * stride + 8 * vc);
     }
   }
+  // Page id of this wave's rows of the tile at key n (page16 only).
+  auto wave_page = [&](int n) -> int {
+    return t.pg[__builtin_amdgcn_readfirstlane(min(n + kRowsPerWave * wave_u, t.last - 1) >> a.page_shift)];
+  };
+  int next_pid = 0;  // page id for the next tile to issue (page16)
   auto issue_tile = [&](int n0, bf16_t* kd) {
     bf16_t* vd = kd + kTileElems;
-    if constexpr (!PAGED) {
-      if (n0 + kBN <= t.last) {  // a full tile: no clamping
-        const bf16_t* kb = t.kbase + (int64_t)n0 * t.kv_stride;
-        const bf16_t* vb = t.vbase + (int64_t)n0 * t.kv_stride;
-#pragma unroll
-        for (int i = 0; i < kRowsPerWave / 4; ++i) {
-          const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;
-          __builtin_amdgcn_global_load_lds(kb + koff[i], (lds_void*)(kd + lrow), 16, 0, 0);
-          __builtin_amdgcn_global_load_lds(vb + voff[i], (lds_void*)(vd + lrow), 16, 0, 0);
-        }
-        return;
+    if (n0 + kBN <= t.last && (!PAGED || page16)) {  // a full tile: no clamping
+      const bf16_t* kb;
+      const bf16_t* vb;
+      if constexpr (PAGED) {
+        const int sh = a.page_shift;
+        const int64_t slot0 = ((int64_t)next_pid << sh) | ((n0 + kRowsPerWave * wave_u) & ((1 << sh) - 1));
+        kb = t.kbase + slot0 * t.per_slot;
+        vb = t.vbase + slot0 * t.per_slot;
+      } else {
+        kb = t.kbase + (int64_t)n0 * t.kv_stride;
+        vb = t.vbase + (int64_t)n0 * t.kv_stride;
       }
+#pragma unroll
+      for (int i = 0; i < kRowsPerWave / 4; ++i) {
+        const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;
+        __builtin_amdgcn_global_load_lds(kb + koff[i], (lds_void*)(kd + lrow), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb + voff[i], (lds_void*)(vd + lrow), 16, 0, 0);
+      }
+      return;
     }
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
@@ -262,13 +283,16 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   const int steps = (t.last + kBN - 1) / kBN;
   const int s_lo = chunk < 0 ? 0 : chunk * steps / a.split_k;
   const int s_hi = chunk < 0 ? steps : (chunk + 1) * steps / a.split_k;
+  if (page16 && s_hi > s_lo) next_pid = wave_page(s_lo * kBN);
   if (s_hi > s_lo) issue_tile(s_lo * kBN, smem0);
+  if (page16 && s_lo + 1 < s_hi) next_pid = wave_page((s_lo + 1) * kBN);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first tile is in LDS
   __syncthreads();
   // One key tile: start loading the next tile into `nxt`, compute from `cur`.
   auto tile_step = [&](int st, const bf16_t* cur, bf16_t* nxt) {
     const int n0 = st * kBN;
     if (st + 1 < s_hi) issue_tile(n0 + kBN, nxt);  // lands while this tile computes
+    if (page16 && st + 2 < s_hi) next_pid = wave_page(n0 + 2 * kBN);  // a tile ahead
     const bf16_t* kt = cur;
     const bf16_t* vt = cur + kTileElems;  // V tile
 
