@@ -243,6 +243,35 @@ int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* ou
 /* Workspace bytes omni_hidream_attend_ws needs at most on the current device. */
 int64_t omni_hidream_workspace_bytes(void);
 
+/* ------------------------------------------------------- host row builder */
+
+/* The engines' `Rows` (crates/omni-qwen3-tts/src/model.rs:266-303,
+ * crates/omni-personaplex/src/model.rs:472-499) in native host code: a step's
+ * rows are pushed one sequence at a time with that sequence's lease (its page
+ * ids) and a range of positions; the builder yields pos, slot, seq, indptr and
+ * pages exactly as Rows::push_seq / Rows::push do. slot of position p is
+ * page_ids[q / page] * page + q % page with q = p, or q = p % ring when ring > 0
+ * (PersonaPlex's CONTEXT). Host memory only; the arrays are the inputs of the
+ * omni_*_rope and omni_*_attend entry points once uploaded. */
+typedef struct omni_attn_rows omni_attn_rows;
+
+#define OMNI_ATTN_ROWS_POS 0
+#define OMNI_ATTN_ROWS_SLOT 1
+#define OMNI_ATTN_ROWS_SEQ 2
+#define OMNI_ATTN_ROWS_INDPTR 3
+#define OMNI_ATTN_ROWS_PAGES 4
+
+/* NULL on a bad argument (omni_attn_last_error says which). */
+omni_attn_rows* omni_attn_rows_new(int page, int ring);
+void omni_attn_rows_free(omni_attn_rows* rows);
+void omni_attn_rows_clear(omni_attn_rows* rows);
+/* Rows first .. first + count - 1 of sequence `seq` with lease pages
+ * page_ids[0 .. npages); OMNI_ATTN_ETABLE if a row's slot is not in the lease. */
+int omni_attn_rows_push(omni_attn_rows* rows, const int32_t* page_ids, int npages, int first, int count, int seq);
+int omni_attn_rows_count(const omni_attn_rows* rows, int* nrows, int* nseqs, int* npages);
+/* One of the arrays (OMNI_ATTN_ROWS_*), valid until the next push / clear / free. */
+const int32_t* omni_attn_rows_get(const omni_attn_rows* rows, int which);
+
 /* ------------------------------------------------------------- library */
 
 /* Library version (major * 10000 + minor * 100 + patch). */

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <new>
 #include <array>
 #include <climits>
 #include <cmath>
@@ -619,4 +620,85 @@ int omni_lm_dep_kv_attend(const void* qkv, void* ws, int step, void* out, int ro
   a.step = step;
   a.scale = scale;
   return short_common(a, omni::kShortDep, "lm_dep_kv_attend", stream);
+}
+
+// ----------------------------------------------------------- host row builder
+
+struct omni_attn_rows {
+  int page;
+  int ring;  // > 0: slot of position p is the lease's slot of p % ring (PersonaPlex)
+  std::vector<int32_t> pos, slot, seq, indptr, pages;
+};
+
+omni_attn_rows* omni_attn_rows_new(int page, int ring) {
+  if (!pow2(page) || ring < 0) {
+    fail(OMNI_ATTN_EINVAL, "rows_new: page=%d (a power of two) ring=%d", page, ring);
+    return nullptr;
+  }
+  omni_attn_rows* r = new (std::nothrow) omni_attn_rows();
+  if (!r) {
+    fail(OMNI_ATTN_EINVAL, "rows_new: out of memory");
+    return nullptr;
+  }
+  r->page = page;
+  r->ring = ring;
+  ok();
+  return r;
+}
+
+void omni_attn_rows_free(omni_attn_rows* r) { delete r; }
+
+void omni_attn_rows_clear(omni_attn_rows* r) {
+  if (!r) return;
+  r->pos.clear();
+  r->slot.clear();
+  r->seq.clear();
+  r->indptr.clear();
+  r->pages.clear();
+}
+
+int omni_attn_rows_push(omni_attn_rows* r, const int32_t* page_ids, int npages, int first, int count, int seq) {
+  if (!r || (npages > 0 && !page_ids) || npages < 0 || first < 0 || count < 0 || seq < 0)
+    return fail(OMNI_ATTN_EINVAL, "rows_push: npages=%d first=%d count=%d seq=%d", npages, first, count, seq);
+  for (int i = 0; i < npages; ++i)
+    if (page_ids[i] < 0) return fail(OMNI_ATTN_ETABLE, "rows_push: page id %d at %d", page_ids[i], i);
+  // Every row's slot must lie in the lease.
+  const int64_t last = count > 0 ? (int64_t)first + count - 1 : -1;
+  const int64_t reach = r->ring > 0 ? std::min<int64_t>(last, r->ring - 1) : last;
+  if (count > 0 && reach / r->page >= npages)
+    return fail(OMNI_ATTN_ETABLE, "rows_push: position %lld needs page %lld of a %d-page lease", (long long)last,
+                (long long)(reach / r->page), npages);
+  if (r->pos.size() + (size_t)count > (size_t)INT32_MAX || r->pages.size() + (size_t)npages > (size_t)INT32_MAX)
+    return fail(OMNI_ATTN_EINVAL, "rows_push: too many rows or pages");
+  if (r->indptr.empty()) r->indptr.push_back(0);
+  for (int i = 0; i < count; ++i) {
+    const int64_t p = (int64_t)first + i;
+    const int64_t q = r->ring > 0 ? p % r->ring : p;
+    r->pos.push_back((int32_t)p);
+    r->slot.push_back((int32_t)((int64_t)page_ids[q / r->page] * r->page + q % r->page));
+    r->seq.push_back(seq);
+  }
+  r->pages.insert(r->pages.end(), page_ids, page_ids + npages);
+  r->indptr.push_back((int32_t)r->pages.size());
+  return ok();
+}
+
+int omni_attn_rows_count(const omni_attn_rows* r, int* rows, int* nseqs, int* npages) {
+  if (!r) return fail(OMNI_ATTN_EINVAL, "rows_count: null builder");
+  if (rows) *rows = (int)r->pos.size();
+  if (nseqs) *nseqs = r->indptr.empty() ? 0 : (int)r->indptr.size() - 1;
+  if (npages) *npages = (int)r->pages.size();
+  return ok();
+}
+
+const int32_t* omni_attn_rows_get(const omni_attn_rows* r, int which) {
+  if (!r) return nullptr;
+  switch (which) {
+    case OMNI_ATTN_ROWS_POS: return r->pos.data();
+    case OMNI_ATTN_ROWS_SLOT: return r->slot.data();
+    case OMNI_ATTN_ROWS_SEQ: return r->seq.data();
+    case OMNI_ATTN_ROWS_INDPTR: return r->indptr.data();
+    case OMNI_ATTN_ROWS_PAGES: return r->pages.data();
+    default: return nullptr;
+  }
 }

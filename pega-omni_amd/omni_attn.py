@@ -47,6 +47,12 @@ EXPORTS = (
     "omni_qwen3_rope_dense",
     "omni_lm_rope",
     "omni_hidream_qk_rope",
+    "omni_attn_rows_new",
+    "omni_attn_rows_free",
+    "omni_attn_rows_clear",
+    "omni_attn_rows_push",
+    "omni_attn_rows_count",
+    "omni_attn_rows_get",
     "omni_attn_version",
     "omni_attn_last_error",
 )
@@ -129,11 +135,22 @@ def load(path: str | None = None):
         "omni_attn_version": [],
         "omni_attn_last_error": [],
     }
+    sig.update({
+        "omni_attn_rows_new": [i32, i32],
+        "omni_attn_rows_free": [P],
+        "omni_attn_rows_clear": [P],
+        "omni_attn_rows_push": [P, P, i32, i32, i32, i32],
+        "omni_attn_rows_count": [P, P, P, P],
+        "omni_attn_rows_get": [P, i32],
+    })
     for name, args in sig.items():
         fn = getattr(L, name)
         fn.argtypes = args
         fn.restype = (ctypes.c_char_p if name == "omni_attn_last_error"
-                      else ctypes.c_int64 if name == "omni_hidream_workspace_bytes" else ctypes.c_int)
+                      else ctypes.c_int64 if name == "omni_hidream_workspace_bytes"
+                      else ctypes.c_void_p if name == "omni_attn_rows_new"
+                      else ctypes.POINTER(ctypes.c_int32) if name == "omni_attn_rows_get"
+                      else None if name in ("omni_attn_rows_free", "omni_attn_rows_clear") else ctypes.c_int)
     _lib = L
     return L
 
@@ -409,3 +426,50 @@ def hidream_attend_ws(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_lo
                                          int(kv_bstride), int(out_bstride), _ptr(workspace), nbytes,
                                          _stream(stream)))
     return out
+
+
+# ------------------------------------------------------------ host row builder
+class Rows:
+    """The engines' ``Rows`` (crates/omni-qwen3-tts/src/model.rs:266-303,
+    crates/omni-personaplex/src/model.rs:472-499) on the native builder:
+    ``push(page_ids, first, count, seq)`` per sequence, then the int32 arrays
+    ``pos``, ``slot``, ``seq``, ``indptr``, ``pages`` (numpy copies)."""
+
+    _WHICH = {"pos": 0, "slot": 1, "seq": 2, "indptr": 3, "pages": 4}
+
+    def __init__(self, page: int = 16, ring: int = 0):
+        h = load().omni_attn_rows_new(page, ring)
+        if not h:
+            raise OmniAttnError(EINVAL, load().omni_attn_last_error().decode())
+        self._h = ctypes.c_void_p(h)
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.omni_attn_rows_free(self._h)
+            self._h = None
+
+    def push(self, page_ids, first: int, count: int, seq: int):
+        import numpy as np
+
+        ids = np.ascontiguousarray(page_ids, dtype=np.int32)
+        _check(load().omni_attn_rows_push(self._h, ids.ctypes.data_as(ctypes.c_void_p), len(ids), first, count, seq))
+
+    def clear(self):
+        load().omni_attn_rows_clear(self._h)
+
+    def counts(self):
+        r, s, p = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        _check(load().omni_attn_rows_count(self._h, ctypes.byref(r), ctypes.byref(s), ctypes.byref(p)))
+        return r.value, s.value, p.value
+
+    def __getattr__(self, name):
+        if name not in Rows._WHICH:
+            raise AttributeError(name)
+        import numpy as np
+
+        rows, seqs, pages = self.counts()
+        n = {"pos": rows, "slot": rows, "seq": rows, "indptr": seqs + 1 if seqs else 0, "pages": pages}[name]
+        if n == 0:
+            return np.zeros(0, np.int32)
+        ptr = load().omni_attn_rows_get(self._h, Rows._WHICH[name])
+        return np.ctypeslib.as_array(ptr, shape=(n,)).copy()
