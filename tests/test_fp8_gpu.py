@@ -93,3 +93,26 @@ def test_fp8_full_config3(oracle):
                      heads, c.scale, 3000, plan, oa.workspace_for(plan))
     torch.cuda.synchronize()
     assert_close(host_bits(out), oracle_fp8(oracle, c, heads), what="fp8 config3")
+
+
+@pytest.mark.parametrize("gh", [0, 1, 4])
+def test_fp8_ragged_prefill_rows(oracle, gh):
+    """PersonaPlex's prefill rows (ragged = 1): several rows of one session at
+    consecutive positions, each seeing min(pos + 1, context) ring slots."""
+    heads = 8
+    p = W.ragged_prefill_case(3, heads, heads, 5, 200, 0, 120, seed=11 + gh, values=None, slack_pages=2)
+    rng = np.random.default_rng(gh)
+    kvf = rng.standard_normal((p.num_pages * 16, 2 * heads, 128), dtype=np.float32)
+    p.kv = W.quantize_fp8_slots(kvf, heads)
+    p.qkv = W.normal_bits(rng, (p.rows, 3 * heads * 128))
+    p.context = 150
+    plan = oa.decode_plan(p.rows, heads, heads, 16, 150, 128)
+    plan.group_heads = gh
+    out = torch.zeros(p.rows, heads * 128, dtype=torch.bfloat16, device="cuda")
+    oa.lm_attend_fp8(dev_bits(p.qkv), torch.from_numpy(p.kv).cuda(), dev_i32(p.pos), dev_i32(p.seq), 1,
+                     dev_i32(p.indptr), dev_i32(p.pages), 16, out, heads, p.scale, p.context, plan,
+                     oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    want = oracle.lm_attend_fp8(p.qkv, p.kv, p.pos, p.seq, 1, p.indptr, p.pages, 16, heads, p.scale, p.context,
+                                nthreads=16)
+    assert_close(host_bits(out), want, what=f"fp8 ragged gh{gh}")
