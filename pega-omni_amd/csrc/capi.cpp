@@ -228,8 +228,7 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   const int G = hq / hk;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: hq/hk=%d not in {1,2,4,8}", G);
-  if (!pow2(page) || page < 4)
-    return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: page=%d is not a power of two >= 4", page);
+  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: page=%d is not a power of two", page);
   if (rows > 0 && (!seq_h || !pos_h)) return fail(OMNI_ATTN_EINVAL, "prefill_plan: null host arrays");
   const int per_tile = omni::kTiledRows / G;  // query positions per tile
   plan->rows = rows;
