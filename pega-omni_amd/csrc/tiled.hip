@@ -37,8 +37,10 @@ constexpr int kWaves = kTiledRows / 32;  // one 32-row query block per wave
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWave = kBN / kWaves;  // K/V tile rows each wave loads
 // LDS per buffer: the K tile then the V tile, each [64 keys][128] bf16 in
-// 256-byte rows, filled straight from global memory (global_load_lds_dwordx4:
-// lane l of a wave's load lands at M0 + 16 l, so one load fills 4 rows). The
+// 256-byte rows, filled straight from global memory by LDS DMA
+// (buffer_load_dwordx4 ... lds for full tiles, global_load_lds_dwordx4 for the
+// clamped last tile: lane l of a wave's load lands at M0 + 16 l, so one load
+// fills 4 rows). The
 // rows are XOR-swizzled for conflict-free operand reads on an LDS of 64 banks
 // x 4 bytes; the swizzle is applied by choosing which global 16-byte chunk
 // each lane loads.
@@ -47,6 +49,39 @@ constexpr int kRowsPerWave = kBN / kWaves;  // K/V tile rows each wave loads
 //   V: 64-byte unit u of row r sits in unit u ^ (r & 3): the 4 rows x 64 bytes
 //      of one phase of a transposing read (ds_read_b64_tr_b16) are disjoint.
 constexpr int kTileElems = kBN * kHead;
+// Buffer resource word 3 for raw (untyped) buffer loads on gfx9-family GPUs.
+constexpr int kBufferFlags = 0x00020000;
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// A raw buffer resource over a wave-uniform base address.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base) {
+  const uint64_t b = (uint64_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)b), __builtin_amdgcn_readfirstlane((int)(b >> 32)), -1,
+               kBufferFlags};
+}
+
+// LDS DMA of 16 bytes per lane into lds + 16 * lane (lds wave-uniform), issued
+// from inline asm: the compiler's wait-count model cannot order an LDS DMA
+// against LDS reads and falls back to lgkmcnt(0) before every LDS operand read
+// while one is in flight. Out of its sight, the reads keep their partial waits;
+// the kernel waits for these loads itself (vmcnt(0) before each tile barrier).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+__device__ __forceinline__ void dma_buffer16(i32x4 rsrc, uint32_t voff, const void* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds_addr(lds))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma_global16(const void* src, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_addr(lds))
+               : "memory", "m0");
+}
 constexpr int kBufElems = 2 * kTileElems;
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -187,7 +222,6 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   // slot l % 16.
   // Keys past `last` repeat the last key (their scores are masked).
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  typedef __attribute__((address_space(3))) void lds_void;
   // Dense sources: within a full tile a lane's rows and chunks are fixed, so
   // its element offsets from the tile's first key are constants (32-bit) and a
   // tile adds one uniform base: loads take a scalar base and a vector offset.
@@ -213,10 +247,15 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     }
   }
   // Page id of this wave's rows of the tile at key n (page16 only).
+  // Loaded as a vector load a tile before use and made scalar only then, so
+  // reading it does not wait for the tile loads issued in between.
+  const __amdgpu_buffer_rsrc_t pg_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(PAGED ? (void*)t.pg : nullptr, 0, -1, kBufferFlags);
   auto wave_page = [&](int n) -> int {
-    return t.pg[__builtin_amdgcn_readfirstlane(min(n + kRowsPerWave * wave_u, t.last - 1) >> a.page_shift)];
+    const int i = __builtin_amdgcn_readfirstlane(min(n + kRowsPerWave * wave_u, t.last - 1) >> a.page_shift);
+    return __builtin_amdgcn_raw_buffer_load_b32(pg_rsrc, 0, 4 * i, 0);
   };
-  int next_pid = 0;  // page id for the next tile to issue (page16)
+  int next_pid = 0;  // page id for the next tile to issue (page16), per lane
   auto issue_tile = [&](int n0, bf16_t* kd) {
     bf16_t* vd = kd + kTileElems;
     if (n0 + kBN <= t.last && (!PAGED || page16)) {  // a full tile: no clamping
@@ -224,21 +263,27 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
       const bf16_t* vb;
       if constexpr (PAGED) {
         const int sh = a.page_shift;
-        const int64_t slot0 = ((int64_t)next_pid << sh) | ((n0 + kRowsPerWave * wave_u) & ((1 << sh) - 1));
+        const int64_t slot0 = ((int64_t)__builtin_amdgcn_readfirstlane(next_pid) << sh) |
+                              ((n0 + kRowsPerWave * wave_u) & ((1 << sh) - 1));
         kb = t.kbase + slot0 * t.per_slot;
         vb = t.vbase + slot0 * t.per_slot;
       } else {
         kb = t.kbase + (int64_t)n0 * t.kv_stride;
         vb = t.vbase + (int64_t)n0 * t.kv_stride;
       }
+      // Buffer loads to LDS: the tile's base in a scalar resource, the
+      // lane's constant byte offsets in VGPRs, no per-lane address math.
+      const i32x4 kr = buffer_rsrc(kb), vr = buffer_rsrc(vb);
 #pragma unroll
       for (int i = 0; i < kRowsPerWave / 4; ++i) {
         const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;
-        __builtin_amdgcn_global_load_lds(kb + koff[i], (lds_void*)(kd + lrow), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vb + voff[i], (lds_void*)(vd + lrow), 16, 0, 0);
+        dma_buffer16(kr, 2 * koff[i], kd + lrow);
+        dma_buffer16(vr, 2 * voff[i], vd + lrow);
       }
       return;
     }
+    // Offsets first, then the loads (the paged offsets need the page ids).
+    int64_t koffs[kRowsPerWave / 4], voffs[kRowsPerWave / 4];
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
       const int row = kRowsPerWave * wave_u + 4 * i + (lane >> 4);
@@ -253,9 +298,14 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
       } else {
         off = (int64_t)key * t.kv_stride;
       }
+      koffs[i] = off + 8 * kc;
+      voffs[i] = off + 8 * vc;
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / 4; ++i) {
       const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;
-      __builtin_amdgcn_global_load_lds(t.kbase + off + 8 * kc, (lds_void*)(kd + lrow), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(t.vbase + off + 8 * vc, (lds_void*)(vd + lrow), 16, 0, 0);
+      dma_global16(t.kbase + koffs[i], kd + lrow);
+      dma_global16(t.vbase + voffs[i], vd + lrow);
     }
   };
 
@@ -334,7 +384,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[mb][e]);
-    mx = fmaxf(mx, xor_lane(mx, 32));
+    {  // lanes l and l ^ 32 hold the two halves of the row's keys
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
     // The running base m moves only when the max grows by more than 8 (log2):
     // p = 2^(s - m) <= 2^8 stays exact in f32 and l, O share the same base,
     // so the result is unchanged while most tiles skip rescaling O.
