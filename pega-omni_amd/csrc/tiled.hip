@@ -67,20 +67,22 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base) {
 // against LDS reads and falls back to lgkmcnt(0) before every LDS operand read
 // while one is in flight. Out of its sight, the reads keep their partial waits;
 // the kernel waits for these loads itself (vmcnt(0) before each tile barrier).
+// M0 (the LDS base of a DMA) is an input operand, so the compiler sets it; the
+// s_nop covers the M0-write-to-DMA hazard.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_void*)p;
 }
 __device__ __forceinline__ void dma_buffer16(i32x4 rsrc, uint32_t voff, const void* lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(voff), "s"(rsrc), "s"(lds_addr(lds))
-               : "memory", "m0");
+               : "v"(voff), "s"(rsrc), "{m0}"(lds_addr(lds))
+               : "memory");
 }
 __device__ __forceinline__ void dma_global16(const void* src, const void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
-               : "v"(src), "s"(lds_addr(lds))
-               : "memory", "m0");
+               : "v"(src), "{m0}"(lds_addr(lds))
+               : "memory");
 }
 constexpr int kBufElems = 2 * kTileElems;
 
