@@ -156,15 +156,21 @@ int omni_attn_gather_kv(const void* kv, int hk, const int32_t* indptr, const int
  * crates/omni-qwen3-tts/src/model.rs:278-289). */
 typedef struct omni_attn_prefill_plan {
   int32_t rows, hq, hk, page;
-  int32_t tiles;     /* query tiles in the work list */
+  int32_t tiles;     /* query tiles (each runs once per kv head) */
   int32_t tile_rows; /* packed (position, head) rows per tile */
   int64_t work_bytes; /* bytes of the int32 work list the caller uploads */
+  int32_t workgroups; /* grid of omni_attn_prefill_run */
+  int32_t reserved;
 } omni_attn_prefill_plan;
 
 /* Host: validate (seq_h, pos_h) for `rows` ragged rows and write the work list
- * into work_h (capacity work_cap int32): 4 int32 per tile (sequence, first
- * row, rows, keys its last row sees), longest tiles first. Returns
- * OMNI_ATTN_EWORKSPACE with plan->work_bytes set when work_h is too small. */
+ * into work_h (capacity work_cap int32): a header of 16 int32 whose entries
+ * 0..8 bound the item ranges of the GPU's 8 XCDs, then 4 int32 per (tile, kv
+ * head) item (sequence, first row, rows, kv head). Items run sequence by
+ * sequence, each kv head's tiles longest first, so the workgroups on one XCD
+ * share one sequence's K/V in that XCD's L2; the XCD ranges have nearly equal
+ * rows x keys. Returns OMNI_ATTN_EWORKSPACE with plan->work_bytes set when
+ * work_h is too small. */
 int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_t* seq_h, const int32_t* pos_h,
                                 int32_t* work_h, int64_t work_cap, omni_attn_prefill_plan* plan);
 

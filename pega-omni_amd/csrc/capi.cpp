@@ -9,6 +9,8 @@
 #include <new>
 #include <array>
 #include <climits>
+#include <unordered_map>
+#include <vector>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -236,37 +238,78 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   plan->hk = hk;
   plan->page = page;
   plan->tile_rows = omni::kTiledRows;
-  // Runs of rows of one sequence at consecutive positions, cut into tiles.
-  int64_t tiles = 0;
+  // Runs of rows of one sequence at consecutive positions, cut into tiles:
+  // (sequence, first row, rows, keys the last row sees).
+  std::vector<std::array<int32_t, 4>> tl;
   for (int n = 0; n < rows;) {
     int e = n + 1;
     if (pos_h[n] < 0) return fail(OMNI_ATTN_ETABLE, "prefill_plan: row %d at negative position %d", n, pos_h[n]);
     while (e < rows && seq_h[e] == seq_h[n] && pos_h[e] == pos_h[e - 1] + 1) ++e;
     for (int f = n; f < e; f += per_tile) {
-      if (work_h && (tiles + 1) * 4 <= work_cap) {
-        const int nq = (e - f) < per_tile ? (e - f) : per_tile;
-        work_h[tiles * 4 + 0] = seq_h[n];
-        work_h[tiles * 4 + 1] = f;
-        work_h[tiles * 4 + 2] = nq;
-        work_h[tiles * 4 + 3] = pos_h[f + nq - 1] + 1;  // keys the tile's last row sees
-      }
-      ++tiles;
+      const int nq = (e - f) < per_tile ? (e - f) : per_tile;
+      tl.push_back({seq_h[n], f, nq, pos_h[f + nq - 1] + 1});
     }
     n = e;
   }
-  if (tiles > INT_MAX / 4) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: too many tiles");
+  const int64_t tiles = (int64_t)tl.size();
+  const int64_t items = tiles * hk;
+  if (items > (INT_MAX - omni::kPrefillWorkHeader) / 4) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: too many tiles");
   plan->tiles = (int32_t)tiles;
-  plan->work_bytes = tiles * 4 * (int64_t)sizeof(int32_t);
-  if (!work_h || tiles * 4 > work_cap)
-    return fail(OMNI_ATTN_EWORKSPACE, "prefill_plan: work list needs %lld int32", (long long)(tiles * 4));
-  // Longest tiles first: causal tiles differ in length by up to the whole
-  // context, and starting the long ones first keeps short ones for the tail.
-  std::vector<std::array<int32_t, 4>> order(tiles);
-  for (int64_t i = 0; i < tiles; ++i)
-    for (int k = 0; k < 4; ++k) order[i][k] = work_h[i * 4 + k];
-  std::stable_sort(order.begin(), order.end(), [](const auto& x, const auto& y) { return x[3] > y[3]; });
-  for (int64_t i = 0; i < tiles; ++i)
-    for (int k = 0; k < 4; ++k) work_h[i * 4 + k] = order[i][k];
+  const int64_t need = omni::kPrefillWorkHeader + 4 * items;
+  plan->work_bytes = need * (int64_t)sizeof(int32_t);
+  plan->workgroups = 0;
+  plan->reserved = 0;
+  if (!work_h || need > work_cap)
+    return fail(OMNI_ATTN_EWORKSPACE, "prefill_plan: work list needs %lld int32", (long long)need);
+  // Item order: sequences by their longest tile, then per sequence each kv
+  // head's tiles, longest first. The workgroups resident on one XCD then work
+  // on one (sequence, kv head) at a time and share its K/V in that XCD's L2,
+  // and each XCD ends on short tiles.
+  std::unordered_map<int32_t, int32_t> longest;
+  for (const auto& t : tl) {
+    auto it = longest.find(t[0]);
+    if (it == longest.end() || it->second < t[3]) longest[t[0]] = t[3];
+  }
+  std::stable_sort(tl.begin(), tl.end(), [&](const auto& x, const auto& y) {
+    const int32_t lx = longest[x[0]], ly = longest[y[0]];
+    if (lx != ly) return lx > ly;
+    if (x[0] != y[0]) return x[0] < y[0];
+    return x[3] > y[3];
+  });
+  int32_t* it = work_h + omni::kPrefillWorkHeader;
+  std::vector<double> cost;
+  cost.reserve(items);
+  for (int64_t b = 0; b < tiles;) {
+    int64_t e = b + 1;
+    while (e < tiles && tl[e][0] == tl[b][0]) ++e;
+    for (int h = 0; h < hk; ++h)
+      for (int64_t i = b; i < e; ++i) {
+        it[0] = tl[i][0];
+        it[1] = tl[i][1];
+        it[2] = tl[i][2];
+        it[3] = h;
+        it += 4;
+        cost.push_back((double)tl[i][2] * tl[i][3]);  // rows x keys of the tile
+      }
+    b = e;
+  }
+  // The 8 XCDs (workgroup i runs on XCD i % 8) take contiguous ranges of
+  // nearly equal cost.
+  double total = 0;
+  for (double c : cost) total += c;
+  int32_t* hdr = work_h;
+  for (int k = 0; k < omni::kPrefillWorkHeader; ++k) hdr[k] = 0;
+  double run = 0;
+  int64_t i = 0;
+  for (int x = 1; x < omni::kXcds; ++x) {
+    const double target = total * x / omni::kXcds;
+    while (i < items && run + 0.5 * cost[i] < target) run += cost[i++];
+    hdr[x] = (int32_t)i;
+  }
+  hdr[omni::kXcds] = (int32_t)items;
+  int32_t widest = 0;
+  for (int x = 0; x < omni::kXcds; ++x) widest = std::max(widest, hdr[x + 1] - hdr[x]);
+  plan->workgroups = widest * omni::kXcds;
   return ok();
 }
 
@@ -292,7 +335,7 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
   a.hq = plan->hq;
   a.hk = plan->hk;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const int rc = omni::launch_prefill(a, plan->tiles, as_stream(stream));
+  const int rc = omni::launch_prefill(a, plan->workgroups, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_run: shape not implemented");
   if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "prefill_run: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();

@@ -78,7 +78,12 @@ constexpr int kTiledRows = 128;
 // Bytes of one partial segment of the tail split: O (f32) and (m, l) per packed row.
 constexpr int64_t kSegmentBytes = (int64_t)kTiledRows * (128 + 2) * 4;  // packed (position, head) query rows per MFMA tile
 
-int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream);
+// Prefill work list: a header of kPrefillWorkHeader int32 (entries 0..8: the
+// item ranges of the 8 XCDs, range x = [h[x], h[x + 1])) then 4 int32 per
+// (tile, kv head) item: sequence, first row, rows, kv head.
+constexpr int kPrefillWorkHeader = 16;
+constexpr int kXcds = 8;
+int launch_prefill(const TiledArgs& a, int workgroups, hipStream_t stream);
 
 // Rotary embedding + K/V scatter (the step before attention).
 struct RopeArgs {

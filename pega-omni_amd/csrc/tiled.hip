@@ -128,8 +128,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
   // DiT, XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
   // contiguous block of work items so the tiles sharing one K/V head (and
   // batch) share that XCD's L2.
-  // Prefill: the work list is longest-first, so items go out in order with
-  // the kv heads of one tile side by side (spread over the XCDs).
+  // Prefill: the work list gives each XCD a range of (tile, kv head) items,
+  // ordered so the workgroups resident on an XCD share one (sequence, kv
+  // head) and its K/V stays in that XCD's L2; workgroup i takes item
+  // start[i % 8] + i / 8 of its XCD's range.
   // DiT tail split: the first split_from items run whole, then every later
   // item runs as split_k key chunks (workgroups dispatched after all whole
   // items, so they fill the last round), each with its own XCD-aware order.
@@ -149,20 +151,25 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items
       idx = a.split_from + u / a.split_k;
       chunk = u % a.split_k;
     }
+  } else if (PAGED) {
+    const int x = blockIdx.x & 7;
+    idx = a.work[x] + (int)(blockIdx.x >> 3);
+    if (idx >= a.work[x + 1]) return;
   } else {
     const int per = (items + 7) >> 3;
-    idx = PAGED ? (int)blockIdx.x : (int)((blockIdx.x & 7) * per + (blockIdx.x >> 3));
+    idx = (int)((blockIdx.x & 7) * per + (blockIdx.x >> 3));
     if (idx >= items) return;
   }
-  const int tile = PAGED ? idx / a.hk : idx % ntiles;
-  const int kvh = PAGED ? idx % a.hk : (idx / ntiles) % a.hk;
+  const int32_t* item = PAGED ? a.work + kPrefillWorkHeader + 4 * idx : nullptr;
+  const int tile = PAGED ? 0 : idx % ntiles;
+  const int kvh = PAGED ? item[3] : (idx / ntiles) % a.hk;
   const int b = PAGED ? 0 : idx / (ntiles * a.hk);
   constexpr int kPos = kBM / G;  // positions per tile
 
   Tile t;
   if constexpr (PAGED) {
-    const int s = a.work[tile * 4 + 0], first = a.work[tile * 4 + 1];
-    t.nq = a.work[tile * 4 + 2];
+    const int s = item[0], first = item[1];
+    t.nq = item[2];
     t.pos = a.pos + first;
     t.q = a.q + (int64_t)first * a.q_stride;
     t.out = a.out + (int64_t)first * a.hq * kHead;
@@ -538,8 +545,8 @@ int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) 
   return 0;
 }
 
-int launch_prefill(const TiledArgs& a, int tiles, hipStream_t stream) {
-  return launch_tiled<true>(a, tiles * a.hk, tiles, stream);
+int launch_prefill(const TiledArgs& a, int workgroups, hipStream_t stream) {
+  return launch_tiled<true>(a, workgroups, 0, stream);
 }
 
 int launch_dit(const TiledArgs& a, int batch, hipStream_t stream) {

@@ -87,6 +87,8 @@ class PrefillPlan(ctypes.Structure):
         ("tiles", ctypes.c_int32),
         ("tile_rows", ctypes.c_int32),
         ("work_bytes", ctypes.c_int64),
+        ("workgroups", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

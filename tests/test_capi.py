@@ -106,6 +106,9 @@ def test_check_table_rejects_bad_tables():
     oa.check_table(c.indptr, c.pages, c.num_pages, pos, None, False, 16, context=int(c.pos[0]) + 1)
 
 
+HEADER = 16  # work-list header: entries 0..8 bound the item ranges of the 8 XCDs
+
+
 def _plan_host(rows, hq, hk, seq, pos):
     L = oa.load()
     plan = oa.PrefillPlan()
@@ -119,28 +122,68 @@ def _plan_host(rows, hq, hk, seq, pos):
                                        pos.ctypes.data_as(ctypes.c_void_p), work.ctypes.data_as(ctypes.c_void_p),
                                        len(work), ctypes.byref(plan))
     assert rc == oa.OK
-    return plan, work.reshape(-1, 4)
+    return plan, work[:HEADER], work[HEADER:].reshape(-1, 4)
 
 
-def test_prefill_plan_tiles_cover_every_row_once():
+def _tiles(pos, items):
+    """Distinct tiles (seq, first, rows, keys of the last row) in first-seen order."""
+    out = []
+    for s, first, n, _ in items:
+        t = (int(s), int(first), int(n), int(pos[first + n - 1]) + 1)
+        if t not in out:
+            out.append(t)
+    return out
+
+
+def test_prefill_plan_items_cover_every_row_and_head_once():
     r = W.ragged_prefill_case(5, 32, 8, 1, 300, 0, 100, seed=4)
-    plan, work = _plan_host(r.rows, 32, 8, r.seq, r.pos)
+    plan, hdr, items = _plan_host(r.rows, 32, 8, r.seq, r.pos)
     per_tile = 128 // 4
-    covered = np.zeros(r.rows, int)
-    assert np.all(np.diff(work[:, 3]) <= 0), "tiles are longest first"
-    for s, first, n, keys in work:
-        assert 1 <= n <= per_tile and keys == r.pos[first + n - 1] + 1
+    covered = np.zeros((r.rows, 8), int)
+    for s, first, n, h in items:
+        assert 1 <= n <= per_tile and 0 <= h < 8
         assert np.all(r.seq[first:first + n] == s)
         assert np.all(np.diff(r.pos[first:first + n]) == 1)
-        covered[first:first + n] += 1
-    assert np.all(covered == 1) and plan.tiles == len(work)
+        covered[first:first + n, h] += 1
+    assert np.all(covered == 1)
+    assert plan.tiles * 8 == len(items)
+    # XCD ranges: increasing, covering every item, and the grid spans the widest.
+    assert hdr[0] == 0 and hdr[8] == len(items) and np.all(np.diff(hdr[:9]) >= 0) and np.all(hdr[9:] == 0)
+    assert plan.workgroups == 8 * int(np.diff(hdr[:9]).max())
+
+
+def test_prefill_plan_groups_sequence_and_kv_head():
+    r = W.ragged_prefill_case(6, 16, 4, 40, 400, 0, 200, seed=5)
+    plan, hdr, items = _plan_host(r.rows, 16, 4, r.seq, r.pos)
+    keys = np.array([r.pos[f + n - 1] + 1 for _, f, n, _ in items])
+    # each (sequence, kv head) is one contiguous run, longest tile first
+    runs = [(int(s), int(h)) for s, _, _, h in items]
+    starts = [i for i in range(len(runs)) if i == 0 or runs[i] != runs[i - 1]]
+    assert len(starts) == len(set(runs)), "a (sequence, kv head) group is split"
+    for a, b in zip(starts, starts[1:] + [len(runs)]):
+        assert np.all(np.diff(keys[a:b]) <= 0)
+    # sequences by their longest tile, descending; kv heads in order within one
+    seqs = [runs[a][0] for a in starts]
+    longest = {s: keys[items[:, 0] == s].max() for s in set(seqs)}
+    order = list(dict.fromkeys(seqs))
+    assert all(longest[x] >= longest[y] for x, y in zip(order, order[1:]))
+    for s in order:
+        assert [runs[a][1] for a in starts if runs[a][0] == s] == list(range(4))
+    # the 8 XCD ranges carry nearly equal rows x keys (within the largest item)
+    cost = items[:, 2].astype(float) * keys
+    per = [cost[hdr[x]:hdr[x + 1]].sum() for x in range(8)]
+    assert max(per) - min(per) <= 2 * cost.max() + 1e-9
 
 
 def test_prefill_plan_breaks_runs_at_position_gaps():
     seq = np.array([0, 0, 0, 1, 1, 0, 0], np.int32)
     pos = np.array([5, 6, 8, 0, 1, 9, 10], np.int32)
-    _, work = _plan_host(7, 4, 4, seq, pos)
-    assert [tuple(w) for w in work] == [(0, 5, 2, 11), (0, 2, 1, 9), (0, 0, 2, 7), (1, 3, 2, 2)]
+    plan, _, items = _plan_host(7, 4, 4, seq, pos)
+    assert plan.tiles == 4
+    # sequence 0's tiles (both of its runs) for kv head 0, longest first, then sequence 1
+    assert _tiles(pos, items) == [(0, 5, 2, 11), (0, 2, 1, 9), (0, 0, 2, 7), (1, 3, 2, 2)]
+    assert [tuple(w) for w in items[:3]] == [(0, 5, 2, 0), (0, 2, 1, 0), (0, 0, 2, 0)]
+    assert [int(h) for h in items[:12, 3]] == [0] * 3 + [1] * 3 + [2] * 3 + [3] * 3
 
 
 def test_rope_entry_points_validate_before_launch():
