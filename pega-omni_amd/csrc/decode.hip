@@ -291,9 +291,16 @@ __device__ __forceinline__ float across_key_rows(float v) {
 // NI load instructions (NI * R keys) per wave and iteration. UP: the R keys of
 // one instruction share a page (page >= R), so its id is a scalar load.
 template <int H, int NI, bool UP>
-__global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a) {
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a, int rows) {
   constexpr int R = 8 / H;
-  const int split = blockIdx.x, kg = blockIdx.y, n = blockIdx.z;
+  // Workgroup i runs on XCD i % 8: the head groups of one (row, split) unit
+  // share an XCD (and the slot's scale lines in its L2), while consecutive
+  // units spread over the XCDs.
+  const int groups = a.hk / H;
+  const int x = blockIdx.x & 7, rest = blockIdx.x >> 3;
+  const int kg = rest % groups, unit = (rest / groups) * 8 + x;
+  const int n = unit / a.splits, split = unit % a.splits;
+  if (n >= rows) return;
   const int s = a.ragged ? a.seq[n] : n;
   const int len = decode_len(a, n, s);
   const int split_len = decode_split_len(a, len);
@@ -468,12 +475,13 @@ static int fp8_heads_per_group(const DecodeArgs& a, int rows) {
 
 template <int H>
 static void launch_fp8_h(const DecodeArgs& a, int rows, hipStream_t stream) {
-  const dim3 grid(a.splits, a.hk / H, rows);
+  const int units = rows * a.splits;
+  const dim3 grid(8 * (a.hk / H) * ((units + 7) / 8));
   constexpr int R = 8 / H;
   if (a.page_shift >= __builtin_ctz(R))
-    decode_split_fp8<H, 4, true><<<grid, kDecodeThreads, 0, stream>>>(a);
+    decode_split_fp8<H, 4, true><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
   else
-    decode_split_fp8<H, 4, false><<<grid, kDecodeThreads, 0, stream>>>(a);
+    decode_split_fp8<H, 4, false><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
 }
 
 static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) {
