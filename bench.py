@@ -433,7 +433,9 @@ def measure_peaks(stream):
     t_lds = timed(lambda: L.omni_peaks_lds(sp, blocks, li, st))
     lds_bytes = blocks * 256 * li * 8 * 16
     buf = torch.empty(4 << 30, dtype=torch.uint8, device="cuda")
-    t_rd = timed(lambda: L.omni_peaks_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), sp, 256 * 16, st))
+    # The best of three grid sizes (nontemporal 16-byte loads, grid-stride).
+    t_rd = min(timed(lambda: L.omni_peaks_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), sp, nb, st))
+               for nb in (1024, 2048, 4096))
     del buf
     return dict(mfma_bf16_tflops=round(mfma, 1), exp_glane_ops=round(lanes / t_exp / 1e9, 1),
                 fma_glane_ops=round(lanes / t_fma / 1e9, 1),

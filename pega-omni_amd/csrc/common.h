@@ -37,6 +37,13 @@ __device__ __forceinline__ void widen8(const uint4& u, float* v) {
 }
 
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// A 16-byte load of data read once (K/V streams): nontemporal, so it streams
+// through the caches instead of displacing reusable lines.
+__device__ __forceinline__ uint4 ldg16_stream(const void* p) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

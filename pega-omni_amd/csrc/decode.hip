@@ -158,9 +158,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
     }
     uint4 kr[8], vr[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = ldg16(kb + off[i]);
+    for (int i = 0; i < 8; ++i) kr[i] = ldg16_stream(kb + off[i]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = ldg16(vb + off[i]);
+    for (int i = 0; i < 8; ++i) vr[i] = ldg16_stream(vb + off[i]);
     if (tb + kStride < t1) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + kStride, i);
@@ -356,8 +356,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
     for (int i = 0; i < NI; ++i) {
       const int t = min(tb + R * i + r, t1 - 1);
       const uint8_t* sp = kvb + (((int64_t)pid[i] << shift) | (t & pmask)) * sb;
-      x.kr[i] = ldg16(sp + koff);
-      x.vr[i] = ldg16(sp + voff);
+      x.kr[i] = ldg16_stream(sp + koff);
+      x.vr[i] = ldg16_stream(sp + voff);
       x.ks[i] = *reinterpret_cast<const float*>(sp + ksoff);
       x.vs[i] = *reinterpret_cast<const float*>(sp + vsoff);
     }

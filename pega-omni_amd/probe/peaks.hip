@@ -58,14 +58,16 @@ __global__ __launch_bounds__(256) void lds_loop(float* sink, int iters) {
   for (int i = threadIdx.x; i < 16384; i += 256) buf[i] = (float)i;
   __syncthreads();
   typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 acc = {0, 0, 0, 0};
   int base = (threadIdx.x & 63) * 4 + (threadIdx.x >> 6) * 2048;
   for (int it = 0; it < iters; ++it) {
     asm volatile("" : "+v"(base));  // the reads stay inside the loop
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc += *reinterpret_cast<const f4*>(buf + ((base + k * 256) & 0x3FFC));
+    for (int k = 0; k < 8; ++k) {
+      const f4 v = *reinterpret_cast<const f4*>(buf + ((base + k * 256) & 0x3FFC));
+      asm volatile("" ::"v"(v));  // consumed without arithmetic, so LDS is the limit
+    }
   }
-  if (acc.x + acc.y + acc.z + acc.w == 1234.5f) sink[threadIdx.x] = acc.x;
+  if (iters < 0) sink[threadIdx.x] = buf[threadIdx.x];
 }
 
 extern "C" {
