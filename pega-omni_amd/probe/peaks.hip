@@ -61,11 +61,11 @@ __global__ __launch_bounds__(256) void lds_loop(float* sink, int iters) {
   int base = (threadIdx.x & 63) * 4 + (threadIdx.x >> 6) * 2048;
   for (int it = 0; it < iters; ++it) {
     asm volatile("" : "+v"(base));  // the reads stay inside the loop
+    f4 v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const f4 v = *reinterpret_cast<const f4*>(buf + ((base + k * 256) & 0x3FFC));
-      asm volatile("" ::"v"(v));  // consumed without arithmetic, so LDS is the limit
-    }
+    for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const f4*>(buf + ((base + k * 256) & 0x3FFC));
+    // Consumed without arithmetic, all 8 in flight together, so LDS is the limit.
+    asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]));
   }
   if (iters < 0) sink[threadIdx.x] = buf[threadIdx.x];
 }
