@@ -379,12 +379,12 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
 
 namespace {
 
-// Workgroups of the tiled kernel resident at once on the current device (two per CU).
+// Workgroups of the tiled kernel resident at once on the current device (one per CU).
 int resident_tiled_groups() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  return 2 * cus;
+  return cus;
 }
 
 }  // namespace

@@ -74,9 +74,10 @@ struct TiledArgs {
   float* ws;
 };
 
-constexpr int kTiledRows = 128;
+// Packed (position, head) query rows per MFMA tile: one 8-wave workgroup, one per CU.
+constexpr int kTiledRows = 256;
 // Bytes of one partial segment of the tail split: O (f32) and (m, l) per packed row.
-constexpr int64_t kSegmentBytes = (int64_t)kTiledRows * (128 + 2) * 4;  // packed (position, head) query rows per MFMA tile
+constexpr int64_t kSegmentBytes = (int64_t)kTiledRows * (128 + 2) * 4;
 
 // Prefill work list: a header of kPrefillWorkHeader int32 (entries 0..8: the
 // item ranges of the 8 XCDs, range x = [h[x], h[x + 1])) then 4 int32 per

@@ -7,7 +7,7 @@
 // kernels/hidream.cu:209-347): row n sees the first *kv_len_at keys, with
 // `causal` only keys 0..n; softmax in base 2 with P rounded to bf16 for P.V.
 //
-// A workgroup (4 waves) owns 128 packed query rows: (128 / G positions) x (the
+// A workgroup (8 waves, one per CU) owns 256 packed query rows: (256 / G positions) x (the
 // G query heads of one K/V head), so one K/V tile in LDS serves G heads. Wave w
 // owns packed rows 32w..32w+31. Keys stream through LDS 64 at a time, double
 // buffered: global loads of tile s+1 are in flight while tile s is computed.
@@ -124,7 +124,7 @@ struct Tile {
 };
 
 template <int G, bool PAGED>
-__global__ __launch_bounds__(kThreads, 2) void tiled_attn(TiledArgs a, int items, int ntiles) {
+__global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items, int ntiles) {
   // DiT, XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
   // contiguous block of work items so the tiles sharing one K/V head (and
   // batch) share that XCD's L2.
@@ -558,7 +558,7 @@ int launch_dit(const TiledArgs& a, int batch, hipStream_t stream) {
   return launch_tiled<false>(a, (int)items, ntiles, stream);
 }
 
-// With `resident` workgroups in flight (two per CU), items - items % resident
+// With `resident` workgroups in flight (one per CU), items - items % resident
 // run whole and the rest each split into resident / (items % resident) key
 // chunks, so the last round is full instead of a fraction.
 void dit_split(const TiledArgs& a, int batch, int resident, int* items, int* split_from, int* split_k) {

@@ -138,7 +138,7 @@ def _tiles(pos, items):
 def test_prefill_plan_items_cover_every_row_and_head_once():
     r = W.ragged_prefill_case(5, 32, 8, 1, 300, 0, 100, seed=4)
     plan, hdr, items = _plan_host(r.rows, 32, 8, r.seq, r.pos)
-    per_tile = 128 // 4
+    per_tile = plan.tile_rows // 4
     covered = np.zeros((r.rows, 8), int)
     for s, first, n, h in items:
         assert 1 <= n <= per_tile and 0 <= h < 8
