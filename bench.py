@@ -150,6 +150,31 @@ def time_steps(run_step, steps, warmup, stream, per_launch=None):
     return ms, launch_ms
 
 
+def graph_step_ms(run_step, steps, warmup, stream):
+    """The step captured once into a HIP graph and replayed, as the engines run
+    decode (one graph per batch bucket): ms per replay over `steps` replays
+    after `warmup`."""
+    import torch
+
+    run_step(stream, None)  # plan state and allocations exist before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run_step(stream, None)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(steps):
+            g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    del g
+    return start.elapsed_time(end) / steps
+
+
 def cpu_decode_baseline(cfg=3, rows=32, min_seconds=10.0, threads=None):
     """The oracle (a C port of the reference math) timed on this host's cores on
     a bounded sample of the decode workload: the first `rows` sessions of one
@@ -468,9 +493,11 @@ def headline_bench(args, stream):
     total_bytes = sum(b.bytes_per_layer)
     log(f"[bench] config {cfg}: {ms:.3f} ms/step, {total_bytes / (ms * 1e-3) / 1e9:.0f} GB/s, "
         f"launch {launch_ms*1e3:.1f} us")
+    g = graph_step_ms(lambda s, e: b.step(s, e), args.steps, args.warmup, stream)
+    log(f"[bench] config {cfg} as a replayed HIP graph: {g:.3f} ms/step")
     c = b.cases[0]
     head = dict(ms=ms, launch_ms=launch_ms, total_bytes=total_bytes, layers=b.layers, sessions=c.rows,
-                heads=f"{c.hq}q/{c.hk}kv", kv_pools=len(b.pools), chunk=b.plan.chunk)
+                heads=f"{c.hq}q/{c.hk}kv", kv_pools=len(b.pools), chunk=b.plan.chunk, graph_ms=g)
     del b
     torch.cuda.empty_cache()
     return head
@@ -528,11 +555,14 @@ def main():
         log("[bench] config 2 decode")
         b2 = DecodeBench(2, args.pools, chunk=args.chunk)
         ms2, l2 = time_steps(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream, per_launch=b2.layers)
+        g2 = graph_step_ms(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream)
         tb = sum(b2.bytes_per_layer)
         extra["config2"] = dict(workload="config2: " + __import__("workloads").CONFIGS[2]["desc"],
                                 ms_per_step=round(ms2, 4), gbs=round(tb / (ms2 * 1e-3) / 1e9, 1),
                                 launch_us=round(l2 * 1e3, 2), chunk=b2.plan.chunk,
-                                frac=round(tb / b2.layers / (l2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+                                frac=round(tb / b2.layers / (l2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                graph_ms_per_step=round(g2, 4), graph_gbs=round(tb / (g2 * 1e-3) / 1e9, 1),
+                                graph_frac=round(tb / (g2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         log(f"[bench] {extra['config2']}")
         del b2
         torch.cuda.empty_cache()
@@ -540,11 +570,13 @@ def main():
         log("[bench] config 3 decode over FP8 E4M3 slots")
         b8 = DecodeBench(3, args.pools, chunk=args.chunk, fp8=True)
         ms8, l8 = time_steps(lambda s, e: b8.step(s, e), args.steps, args.warmup, stream, per_launch=b8.layers)
+        g8 = graph_step_ms(lambda s, e: b8.step(s, e), args.steps, args.warmup, stream)
         tb = sum(b8.bytes_per_layer)
         extra["config3_fp8"] = dict(workload="config3 over PersonaPlex FP8 E4M3 slots (8448 B per slot)",
                                     ms_per_step=round(ms8, 4), gbs=round(tb / (ms8 * 1e-3) / 1e9, 1),
                                     launch_us=round(l8 * 1e3, 2), chunk=b8.plan.chunk,
-                                    frac=round(tb / b8.layers / (l8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+                                    frac=round(tb / b8.layers / (l8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                    graph_ms_per_step=round(g8, 4), graph_gbs=round(tb / (g8 * 1e-3) / 1e9, 1))
         log(f"[bench] {extra['config3_fp8']}")
         del b8
         torch.cuda.empty_cache()
@@ -612,7 +644,9 @@ def main():
             "launch_us": round(launch_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
-        "extra": extra,
+        "extra": dict(extra, config3_graph=dict(
+            ms_per_step=round(head["graph_ms"], 4), gbs=round(total_bytes / (head["graph_ms"] * 1e-3) / 1e9, 1),
+            note="the same step captured once as a HIP graph and replayed (the engines' per-bucket graphs)")),
     }
     print(json.dumps(out), flush=True)
 
