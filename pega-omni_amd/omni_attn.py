@@ -200,12 +200,11 @@ def decode_plan(rows: int, hq: int, hk: int, page: int, max_len: int, chunk: int
 
 
 def workspace_for(plan, device="cuda"):
-    """Device workspace for a plan (None when the plan needs none), zero-filled
-    as the decode kernels require before its first use."""
+    """Device workspace for a plan (None when the plan needs none)."""
     import torch
 
     n = int(plan.workspace_bytes)
-    return torch.zeros(n, dtype=torch.uint8, device=device) if n > 0 else None
+    return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
 
 
 def check_table(indptr_h, pages_h, num_pages, pos_h=None, seq_h=None, ragged=False, page=16, context=0):
