@@ -55,11 +55,12 @@ constexpr int kBufferFlags = 0x00020000;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-// A raw buffer resource over a wave-uniform base address.
-__device__ __forceinline__ i32x4 buffer_rsrc(const void* base) {
+// A raw buffer resource over a wave-uniform base address, `bytes` long:
+// loads at offsets past it return zeros without touching memory.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int bytes = -1) {
   const uint64_t b = (uint64_t)base;
-  return i32x4{__builtin_amdgcn_readfirstlane((int)b), __builtin_amdgcn_readfirstlane((int)(b >> 32)), -1,
-               kBufferFlags};
+  return i32x4{__builtin_amdgcn_readfirstlane((int)b), __builtin_amdgcn_readfirstlane((int)(b >> 32)),
+               __builtin_amdgcn_readfirstlane(bytes), kBufferFlags};
 }
 
 // LDS DMA of 16 bytes per lane into lds + 16 * lane (lds wave-uniform), issued
@@ -267,9 +268,16 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   int next_pid = 0;  // page id for the next tile to issue (page16), per lane
   auto issue_tile = [&](int n0, bf16_t* kd) {
     bf16_t* vd = kd + kTileElems;
-    if (n0 + kBN <= t.last && (!PAGED || page16)) {  // a full tile: no clamping
+    if (!PAGED || page16) {
+      // Rows past `last` (the key tile's tail) fall outside the buffer
+      // range and read as zeros: masked scores and zero V rows, so they add
+      // nothing, and no slot past the sequence's keys is read.
       const bf16_t* kb;
       const bf16_t* vb;
+      const int first = PAGED ? n0 + kRowsPerWave * wave_u : n0;  // key of this lane's row 0
+      const int rows = min(max(t.last - first, 0), PAGED ? kRowsPerWave : kBN);
+      const int64_t stride_bytes = 2 * (PAGED ? t.per_slot : t.kv_stride);
+      const int bytes = rows == (PAGED ? kRowsPerWave : kBN) ? -1 : (int)(rows * stride_bytes);
       if constexpr (PAGED) {
         const int sh = a.page_shift;
         const int64_t slot0 = ((int64_t)__builtin_amdgcn_readfirstlane(next_pid) << sh) |
@@ -282,7 +290,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
       }
       // Buffer loads to LDS: the tile's base in a scalar resource, the
       // lane's constant byte offsets in VGPRs, no per-lane address math.
-      const i32x4 kr = buffer_rsrc(kb), vr = buffer_rsrc(vb);
+      const i32x4 kr = buffer_rsrc(kb, bytes), vr = buffer_rsrc(vb, bytes);
 #pragma unroll
       for (int i = 0; i < kRowsPerWave / 4; ++i) {
         const int lrow = (kRowsPerWave * wave_u + 4 * i) * kHead;

@@ -155,3 +155,40 @@ def test_prefill_page_sizes(oracle, page):
     above (one scalar page id per wave of a full tile)."""
     c = W.ragged_prefill_case(3, 32, 8, 40, 260, 0, 150, page=page, seed=page)
     assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill page {page}")
+
+
+BF16_NAN = 0x7FC0
+
+
+def test_prefill_reads_no_slot_past_its_keys(oracle):
+    """Every cache slot no row may see holds NaN, including the rest of each
+    sequence's last page: the tail tile must not read them into P.V."""
+    c = W.ragged_prefill_case(4, 32, 8, 30, 300, 0, 150, seed=21)
+    seen = np.zeros(c.kv.shape[0], bool)
+    for s in range(len(c.indptr) - 1):
+        rows = c.seq == s
+        if not rows.any():
+            continue
+        keys = np.arange(int(c.pos[rows].max()) + 1)
+        pg = c.pages[c.indptr[s]:c.indptr[s + 1]]
+        seen[pg[keys // c.page] * c.page + keys % c.page] = True
+    assert (~seen).any() and any((int(c.pos[c.seq == s].max()) + 1) % 64 for s in np.unique(c.seq))
+    c.kv = c.kv.copy()
+    c.kv[~seen] = BF16_NAN
+    assert_close(run_prefill(c), oracle_paged(oracle, c), what="prefill with NaN past the keys")
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_dit_reads_no_key_past_kv_len(oracle, causal):
+    """K and V rows past *kv_len_at hold NaN; the partial last key tile must
+    not read them into P.V."""
+    c = W.dense_case(32, 8, 200, 400, causal, seed=22)
+    c.k, c.v = c.k.copy(), c.v.copy()
+    c.k[:, 259:] = BF16_NAN
+    c.v[:, 259:] = BF16_NAN
+    q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
+    out = torch.zeros(c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    kvl = dev_i32(np.array([259], np.int32))
+    oa.hidream_attend(q, k, v, out, c.q_len, kvl, c.q_stride, causal, c.scale_log2, c.hq, c.hk)
+    torch.cuda.synchronize()
+    assert_close(host_bits(out), oracle_dense(oracle, c, kv_len=259), what=f"kv_len 259 with NaN past it, c{causal}")
