@@ -71,3 +71,16 @@ class DevPaged:
                             self.out, c.hq, c.hk, c.scale, plan, ws)
         torch.cuda.synchronize()
         return host_bits(self.out)
+
+
+def seen_slots(c):
+    """Mask of the cache slots some row of a paged case reads (keys 0..len-1 of
+    its sequence through the page table)."""
+    seen = np.zeros(c.kv.shape[0], bool)
+    lens = c.lens()
+    for n in range(c.rows):
+        s = int(c.seq[n]) if c.ragged else n
+        keys = np.arange(int(lens[n]))
+        pg = c.pages[c.indptr[s]:c.indptr[s + 1]]
+        seen[pg[keys // c.page] * c.page + keys % c.page] = True
+    return seen

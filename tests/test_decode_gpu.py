@@ -164,3 +164,17 @@ def test_full_config_parity(oracle, cfg):
     got = d.decode(max_len=max_len, lm=cfg == 3)
     want = oracle_out(oracle, c, threads=16)
     assert_close(got, want, what=f"config{cfg}")
+
+
+@pytest.mark.parametrize("chunk", [0, 128])
+def test_reads_no_slot_past_the_keys(oracle, chunk):
+    """Every slot no row reads holds NaN (the rest of each last page and the
+    pool's slack): clamped tail keys must not bring them into P.V."""
+    from gpu_util import seen_slots
+
+    c = W.paged_decode_case(9, 16, 8, 1, 300, seed=31, slack_pages=4)
+    seen = seen_slots(c)
+    assert (~seen).any()
+    c.kv = c.kv.copy()
+    c.kv[~seen] = 0x7FC0  # bf16 NaN
+    assert_close(DevPaged(c).decode(chunk=chunk), oracle_out(oracle, c), what=f"NaN past the keys chunk={chunk}")

@@ -116,3 +116,15 @@ def test_fp8_ragged_prefill_rows(oracle, gh):
     want = oracle.lm_attend_fp8(p.qkv, p.kv, p.pos, p.seq, 1, p.indptr, p.pages, 16, heads, p.scale, p.context,
                                 nthreads=16)
     assert_close(host_bits(out), want, what=f"fp8 ragged gh{gh}")
+
+
+def test_fp8_reads_no_slot_past_the_keys(oracle):
+    """FP8 slots no row reads are all-ones bytes (E4M3 NaN values, NaN scales)."""
+    from gpu_util import seen_slots
+
+    c = W.fp8_ring_case(9, 8, 1, 400, 300, seed=32, slack_pages=4)
+    seen = seen_slots(c)
+    assert (~seen).any()
+    c.kv = c.kv.copy()
+    c.kv[~seen] = 0xFF
+    assert_close(run_fp8(c, 8, 128), oracle_fp8(oracle, c, 8), what="fp8 NaN past the keys")
