@@ -235,18 +235,18 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   // Dense sources: within a full tile a lane's rows and chunks are fixed, so
   // its element offsets from the tile's first key are constants (32-bit) and a
   // tile adds one uniform base: loads take a scalar base and a vector offset.
-  // Paged sources with page >= 16: a wave's 16 rows of a tile are 16
-  // consecutive keys of one page, so a full tile needs one (scalar) page id
-  // per wave, read a tile ahead, and the rows are consecutive slots.
-  const bool page16 = PAGED && a.page_shift >= 4;
-  // Element offsets of this lane's rows from the first row of a wave's block
-  // of 16 (dense: from the tile's first key): constants within full tiles.
+  // Paged sources with page >= kRowsPerWave: a wave's rows of a tile are
+  // consecutive keys of one page, so a tile needs one (scalar) page id per
+  // wave, read a tile ahead, and the rows are consecutive slots.
+  const bool page_wave = PAGED && (1 << a.page_shift) >= kRowsPerWave;
+  // Element offsets of this lane's rows from the first row of the wave's
+  // block (dense: from the tile's first key): constants for every tile.
   uint32_t koff[kRowsPerWave / 4], voff[kRowsPerWave / 4];
   {
     const int64_t stride = PAGED ? t.per_slot : t.kv_stride;
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 4; ++i) {
-      const int wrow = 4 * i + (lane >> 4);  // row within the wave's 16
+      const int wrow = 4 * i + (lane >> 4);  // row within the wave's block
       const int row = kRowsPerWave * wave_u + wrow;
       const int cs = lane & 15;
       const int kc = cs ^ (row & 15);
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
       voff[i] = (uint32_t)(r0 * stride + 8 * vc);
     }
   }
-  // Page id of this wave's rows of the tile at key n (page16 only).
+  // Page id of this wave's rows of the tile at key n (page_wave only).
   // Loaded as a vector load a tile before use and made scalar only then, so
   // reading it does not wait for the tile loads issued in between.
   const __amdgpu_buffer_rsrc_t pg_rsrc =
@@ -265,10 +265,10 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     const int i = __builtin_amdgcn_readfirstlane(min(n + kRowsPerWave * wave_u, t.last - 1) >> a.page_shift);
     return __builtin_amdgcn_raw_buffer_load_b32(pg_rsrc, 0, 4 * i, 0);
   };
-  int next_pid = 0;  // page id for the next tile to issue (page16), per lane
+  int next_pid = 0;  // page id for the next tile to issue (page_wave), per lane
   auto issue_tile = [&](int n0, bf16_t* kd) {
     bf16_t* vd = kd + kTileElems;
-    if (!PAGED || page16) {
+    if (!PAGED || page_wave) {
       // Rows past `last` (the key tile's tail) fall outside the buffer
       // range and read as zeros: masked scores and zero V rows, so they add
       // nothing, and no slot past the sequence's keys is read.
@@ -350,16 +350,16 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   const int steps = (t.last + kBN - 1) / kBN;
   const int s_lo = chunk < 0 ? 0 : chunk * steps / a.split_k;
   const int s_hi = chunk < 0 ? steps : (chunk + 1) * steps / a.split_k;
-  if (page16 && s_hi > s_lo) next_pid = wave_page(s_lo * kBN);
+  if (page_wave && s_hi > s_lo) next_pid = wave_page(s_lo * kBN);
   if (s_hi > s_lo) issue_tile(s_lo * kBN, smem0);
-  if (page16 && s_lo + 1 < s_hi) next_pid = wave_page((s_lo + 1) * kBN);
+  if (page_wave && s_lo + 1 < s_hi) next_pid = wave_page((s_lo + 1) * kBN);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first tile is in LDS
   __syncthreads();
   // One key tile: start loading the next tile into `nxt`, compute from `cur`.
   auto tile_step = [&](int st, const bf16_t* cur, bf16_t* nxt) {
     const int n0 = st * kBN;
     if (st + 1 < s_hi) issue_tile(n0 + kBN, nxt);  // lands while this tile computes
-    if (page16 && st + 2 < s_hi) next_pid = wave_page(n0 + 2 * kBN);  // a tile ahead
+    if (page_wave && st + 2 < s_hi) next_pid = wave_page(n0 + 2 * kBN);  // a tile ahead
     const bf16_t* kt = cur;
     const bf16_t* vt = cur + kTileElems;  // V tile
 

@@ -149,10 +149,10 @@ def test_dit_tail_split_config5_matches_unsplit(oracle):
     del sub
 
 
-@pytest.mark.parametrize("page", [1, 2, 4, 64])
+@pytest.mark.parametrize("page", [1, 2, 4, 8, 64])
 def test_prefill_page_sizes(oracle, page):
-    """The paged tile loader at pages below 16 (one page id per key row) and
-    above (one scalar page id per wave of a full tile)."""
+    """The paged tile loader at pages below a wave's 8 rows of a tile (one page
+    id per key row) and from 8 up (one scalar page id per wave and tile)."""
     c = W.ragged_prefill_case(3, 32, 8, 40, 260, 0, 150, page=page, seed=page)
     assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill page {page}")
 
