@@ -1,8 +1,9 @@
-"""A whole decode step captured once in a HIP graph, as the engines capture one
-per batch bucket, and replayed with new positions, slots and inputs: rotary +
-K/V scatter then attention (bf16 qwen3 path, FP8 lm path). Every replay must
-equal the same step run eagerly, bit for bit (the same kernels on the same
-inputs), with eager work and synchronisations between replays."""
+"""A whole step captured once in a HIP graph, as the engines capture one per
+batch bucket, and replayed with new positions, slots, key counts and inputs:
+rotary + K/V scatter then attention (bf16 qwen3 decode, FP8 lm decode, and the
+HiDream DiT step with the tail-split workspace). Every replay must equal the
+same step run eagerly, bit for bit (the same kernels on the same inputs), with
+eager work and synchronisations between replays."""
 import numpy as np
 import pytest
 import torch
@@ -119,3 +120,58 @@ def test_lm_fp8_step_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(got_out.view(torch.int16), out.view(torch.int16)), f"replay {rep}: attention output"
         assert torch.equal(got_kv, kv), f"replay {rep}: FP8 scatter"
+
+
+def test_dit_step_graph_replays():
+    """HiDream's rotary + K/V write then the batched attention with the tail
+    split (workspace + merge), captured once and replayed with new inputs and
+    new key counts through *kv_len_at, as the diffusion loop replays one graph
+    per step."""
+    hq, hk, rows, text = 32, 8, 300, 100
+    slots_n = text + rows
+    c = W.rope_case("hidream", rows, hq, hk, seed=5, pos_hi=4352)
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    ld = c.ld
+    src = torch.randn(rows, ld, device="cuda", generator=gen).to(torch.bfloat16)
+    k0 = torch.randn(slots_n, hk * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    v0 = torch.randn(slots_n, hk * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    qn = (1 + 0.1 * torch.randn(128, device="cuda", generator=gen)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(128, device="cuda", generator=gen)).to(torch.bfloat16)
+    qkv, kc, vc = torch.empty_like(src), k0.clone(), v0.clone()
+    out = torch.zeros(rows, hq * 128, dtype=torch.bfloat16, device="cuda")
+    pos = dev_i32(c.pos)
+    slots = dev_i32(text + np.arange(rows, dtype=np.int32))  # image rows after the text keys
+    kvl = dev_i32(np.array([slots_n], np.int32))
+    ws = oa.hidream_workspace()
+    scale_log2 = 128 ** -0.5 * 1.4426950408889634
+
+    def step(s):
+        qkv.copy_(src)
+        oa.hidream_qk_rope(qkv, ld, qn, kn, pos, slots, kc, vc, rows, hq, hk, 20, 1e-6, 1e4, s)
+        oa.hidream_attend_ws(qkv, kc, vc, out, rows, kvl, ld, 0, scale_log2, hq, hk, 1, rows * ld,
+                             slots_n * hk * 128, rows * hq * 128, ws, s)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(s)  # warm
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step(s)
+    for rep, n_keys in enumerate((slots_n, 350, 257, 129)):
+        src.copy_(torch.randn(src.shape, device="cuda", generator=gen).to(torch.bfloat16))
+        kvl.copy_(dev_i32(np.array([n_keys], np.int32)))
+        kc.copy_(k0), vc.copy_(v0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got_out, got_k, got_q = out.clone(), kc.clone(), qkv.clone()
+        kc.copy_(k0), vc.copy_(v0)
+        out.zero_()
+        step(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        assert torch.equal(got_out.view(torch.int16), out.view(torch.int16)), f"replay {rep}: attention output"
+        assert torch.equal(got_k.view(torch.int16), kc.view(torch.int16)), f"replay {rep}: K cache"
+        assert torch.equal(got_q.view(torch.int16), qkv.view(torch.int16)), f"replay {rep}: rotated q"
