@@ -9,15 +9,15 @@
 //
 // A workgroup (8 waves, one per CU) owns 256 packed query rows: (256 / G positions) x (the
 // G query heads of one K/V head), so one K/V tile in LDS serves G heads. Wave w
-// owns packed rows 32w..32w+31. Keys stream through LDS 64 at a time, double
+// owns packed rows 32w..32w+31. Keys stream through LDS kBN = 128 at a time, double
 // buffered: global loads of tile s+1 are in flight while tile s is computed.
 //
 // Per wave and key tile, on v_mfma_f32_32x32x16_bf16:
-//   S^T (64 keys x 32 rows) = K (64 x 128) . Q^T (128 x 32): 2 x 8 MFMAs,
+//   S^T (128 keys x 32 rows) = K (128 x 128) . Q^T (128 x 32): 4 x 8 MFMAs,
 //     K from LDS as the A operand, Q held in registers as the B operand.
 //     In the 32x32 accumulator a lane holds one query column (lane % 32) and 16
 //     keys, so the row max and sum are lane-local plus one exchange with lane ^ 32.
-//   O^T (128 dims x 32 rows) += V^T (128 x 64) . P^T (64 x 32): 4 x 4 MFMAs.
+//   O^T (128 dims x 32 rows) += V^T (128 x 128) . P^T (128 x 32): 4 x 8 MFMAs.
 //     P^T's B operand is the S accumulator itself (rounded to bf16): lane half h
 //     of K-step ks holds keys 16 ks + 4 h + {0..3, 8..11}. V stays row-major in
 //     LDS and the V^T operand at exactly those keys comes from two transposing
@@ -32,11 +32,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = kTiledRows;  // packed query rows per workgroup
-constexpr int kBN = 64;          // keys per tile
+constexpr int kBN = 128;         // keys per tile
+constexpr int kMB = kBN / 32;    // 32-key blocks per tile
 constexpr int kWaves = kTiledRows / 32;  // one 32-row query block per wave
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWave = kBN / kWaves;  // K/V tile rows each wave loads
-// LDS per buffer: the K tile then the V tile, each [64 keys][128] bf16 in
+// LDS per buffer: the K tile then the V tile, each [128 keys][128] bf16 in
 // 256-byte rows, filled straight from global memory by LDS DMA
 // (buffer_load_dwordx4 ... lds for full tiles, global_load_lds_dwordx4 for the
 // clamped last tile: lane l of a wave's load lands at M0 + 16 l, so one load
@@ -363,18 +364,18 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     const bf16_t* kt = cur;
     const bf16_t* vt = cur + kTileElems;  // V tile
 
-    // S^T = K . Q^T for keys n0 .. n0 + 63: two interleaved MFMA chains
-    // (key blocks mb = 0, 1) over the 8 K-steps, with the K fragments read
+    // S^T = K . Q^T for keys n0 .. n0 + kBN - 1: kMB interleaved MFMA chains
+    // (32-key blocks mb) over the 8 K-steps, with the K fragments read
     // from LDS two K-steps ahead of use; the stages are pinned in this order.
-    f32x16 sc[2];
+    f32x16 sc[kMB];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) sc[mb][e] = 0.f;
-    uint4 kf[8][2];
+    uint4 kf[8][kMB];
     auto read_k = [&](int kk) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) kf[kk][mb] = *reinterpret_cast<const uint4*>(kt + (k_lane ^ (16 * kk)) + mb * 4096);
+      for (int mb = 0; mb < kMB; ++mb) kf[kk][mb] = *reinterpret_cast<const uint4*>(kt + (k_lane ^ (16 * kk)) + mb * 4096);
     };
     read_k(0);
     read_k(1);
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < kMB; ++mb)
         sc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf[kk][mb]), qf[kk], sc[mb], 0, 0, 0);
       if (kk + 2 < 8) read_k(kk + 2);
       __builtin_amdgcn_sched_barrier(0);
@@ -391,14 +392,14 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     // Register e of block mb is key n0 + 32 mb + 8 (e / 4) + 4 h + e % 4.
     if (__any(n0 + kBN > lim)) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           if (n0 + 32 * mb + 8 * (e >> 2) + 4 * h + (e & 3) >= lim) sc[mb][e] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[mb][e]);
     {  // lanes l and l ^ 32 hold the two halves of the row's keys
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     const float base = m == -INFINITY ? 0.f : m;
     float psum = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         sc[mb][e] = fast_exp2(fmaf(sc[mb][e], sl2, -base));
@@ -432,7 +433,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
 
     // O^T += V^T . P^T: K-step ks covers keys 16 ks + 4 h + {0..3, 8..11}.
 #pragma unroll
-    for (int ks_ = 0; ks_ < 4; ++ks_) {
+    for (int ks_ = 0; ks_ < 2 * kMB; ++ks_) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = sc[ks_ >> 1][8 * (ks_ & 1) + e];

@@ -151,8 +151,8 @@ def test_dit_tail_split_config5_matches_unsplit(oracle):
 
 @pytest.mark.parametrize("page", [1, 2, 4, 8, 64])
 def test_prefill_page_sizes(oracle, page):
-    """The paged tile loader at pages below a wave's 8 rows of a tile (one page
-    id per key row) and from 8 up (one scalar page id per wave and tile)."""
+    """The paged tile loader at pages below a wave's 16 rows of a tile (one
+    page id per key row) and from 16 up (one scalar page id per wave and tile)."""
     c = W.ragged_prefill_case(3, 32, 8, 40, 260, 0, 150, page=page, seed=page)
     assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill page {page}")
 
