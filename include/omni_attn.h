@@ -278,6 +278,18 @@ int omni_attn_rows_count(const omni_attn_rows* rows, int* nrows, int* nseqs, int
 /* One of the arrays (OMNI_ATTN_ROWS_*), valid until the next push / clear / free. */
 const int32_t* omni_attn_rows_get(const omni_attn_rows* rows, int which);
 
+/* Host: HiDream-O1's row arrays for hidream_qk_rope and hidream_attend
+ * (crates/omni-hidream-o1/src/model.rs:123-160, prompt.rs:71-80). The prompt's
+ * `causal` text rows: text_pos[k] = (k, k, k), text_slots[k] = k. The
+ * generation rows, rows = 1 + grid_rows * grid_cols of them: the timestep slot
+ * at text position `causal`, then the patches in raster order at
+ * (image_position, image_position + i, image_position + j); gen_slots =
+ * causal .. causal + rows - 1, and *step_kv = causal + rows keys. Positions
+ * are [n][3] int32. Any output may be null. HiDream-O1's image_position is
+ * 4096 (crates/omni-hidream-o1/src/config.rs:16). */
+int omni_hidream_rows(int causal, int grid_rows, int grid_cols, int image_position, int32_t* text_pos,
+                      int32_t* text_slots, int32_t* gen_pos, int32_t* gen_slots, int32_t* step_kv);
+
 /* ------------------------------------------------------------- library */
 
 /* Library version (major * 10000 + minor * 100 + patch). */

@@ -733,6 +733,34 @@ int omni_attn_rows_count(const omni_attn_rows* r, int* rows, int* nseqs, int* np
   return ok();
 }
 
+int omni_hidream_rows(int causal, int grid_rows, int grid_cols, int image_position, int32_t* text_pos,
+                      int32_t* text_slots, int32_t* gen_pos, int32_t* gen_slots, int32_t* step_kv) {
+  if (causal < 1 || grid_rows < 1 || grid_cols < 1)
+    return fail(OMNI_ATTN_EINVAL, "hidream_rows: causal=%d grid=%dx%d", causal, grid_rows, grid_cols);
+  const int64_t patches = (int64_t)grid_rows * grid_cols, rows = 1 + patches;
+  if (causal + rows > INT_MAX || (int64_t)image_position + std::max(grid_rows, grid_cols) > INT_MAX ||
+      image_position < 0)
+    return fail(OMNI_ATTN_EINVAL, "hidream_rows: positions or slots overflow int32");
+  for (int k = 0; k < causal; ++k) {
+    if (text_pos) text_pos[3 * k] = text_pos[3 * k + 1] = text_pos[3 * k + 2] = k;
+    if (text_slots) text_slots[k] = k;
+  }
+  if (gen_pos) {
+    gen_pos[0] = gen_pos[1] = gen_pos[2] = causal;  // the timestep slot at the last text position
+    int64_t n = 1;
+    for (int i = 0; i < grid_rows; ++i)
+      for (int j = 0; j < grid_cols; ++j, ++n) {
+        gen_pos[3 * n] = image_position;
+        gen_pos[3 * n + 1] = image_position + i;
+        gen_pos[3 * n + 2] = image_position + j;
+      }
+  }
+  if (gen_slots)
+    for (int64_t n = 0; n < rows; ++n) gen_slots[n] = (int32_t)(causal + n);
+  if (step_kv) *step_kv = (int32_t)(causal + rows);
+  return ok();
+}
+
 const int32_t* omni_attn_rows_get(const omni_attn_rows* r, int which) {
   if (!r) return nullptr;
   switch (which) {

@@ -34,6 +34,7 @@ EXPORTS = (
     "omni_attn_check_table",
     "omni_attn_gather_kv",
     "omni_attn_prefill_plan_init",
+    "omni_hidream_rows",
     "omni_attn_prefill_run",
     "omni_hidream_attend",
     "omni_hidream_attend_batched",
@@ -121,6 +122,7 @@ def load(path: str | None = None):
         "omni_attn_check_table": [P, i32, P, i32, P, P, i32, i32, i32, i32],
         "omni_attn_gather_kv": [P, i32, P, P, i32, P, P, P, i32, P, P],
         "omni_attn_prefill_plan_init": [i32, i32, i32, i32, P, P, P, i64, pplan],
+        "omni_hidream_rows": [i32, i32, i32, i32, P, P, P, P, P],
         "omni_attn_prefill_run": [pplan, P, P, P, P, P, P, P, f32, P, P],
         "omni_hidream_attend": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, P],
         "omni_hidream_attend_batched": [P, P, P, P, i32, P, i32, i32, f32, i32, i32, i32, i64, i64, i64, P],
@@ -475,3 +477,20 @@ class Rows:
             return np.zeros(0, np.int32)
         ptr = load().omni_attn_rows_get(self._h, Rows._WHICH[name])
         return np.ctypeslib.as_array(ptr, shape=(n,)).copy()
+
+
+def hidream_rows(causal, grid, image_position=4096):
+    """HiDream-O1's host row arrays (``model.rs:123-160``): (text_pos [causal][3],
+    text_slots, gen_pos [rows][3], gen_slots, step_kv) as numpy int32."""
+    import numpy as np
+
+    rows = 1 + grid[0] * grid[1]
+    tp = np.zeros((causal, 3), np.int32)
+    ts = np.zeros(causal, np.int32)
+    gp = np.zeros((rows, 3), np.int32)
+    gs = np.zeros(rows, np.int32)
+    kv = np.zeros(1, np.int32)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    _check(load().omni_hidream_rows(causal, grid[0], grid[1], image_position, ptr(tp), ptr(ts), ptr(gp), ptr(gs),
+                                    ptr(kv)))
+    return tp, ts, gp, gs, int(kv[0])

@@ -71,3 +71,29 @@ def test_builder_reproduces_the_workload_tables():
         r2.push(p.pages[p.indptr[s]:p.indptr[s + 1]], first, n, s)
     assert np.array_equal(r2.pos, p.pos) and np.array_equal(r2.seq, p.seq)
     assert np.array_equal(r2.indptr, p.indptr) and np.array_equal(r2.pages, p.pages)
+
+
+def test_hidream_rows_follow_the_prompt_layout():
+    """HiDream-O1's prefill rows (model.rs:123-160, prompt.rs:71-80): text row
+    k at (k, k, k) in slot k; the timestep slot at text position `causal`;
+    patch (i, j) at (4096, 4096 + i, 4096 + j) in raster order; generation
+    slots after the text slots; the step sees causal + rows keys."""
+    tp, ts, gp, gs, kv = oa.hidream_rows(3, (2, 3))
+    assert tp.tolist() == [[0, 0, 0], [1, 1, 1], [2, 2, 2]] and ts.tolist() == [0, 1, 2]
+    assert gp.tolist() == [[3, 3, 3],
+                           [4096, 4096, 4096], [4096, 4096, 4097], [4096, 4096, 4098],
+                           [4096, 4097, 4096], [4096, 4097, 4097], [4096, 4097, 4098]]
+    assert gs.tolist() == [3, 4, 5, 6, 7, 8, 9] and kv == 10
+    # a 64 x 64 grid at another image origin
+    tp, ts, gp, gs, kv = oa.hidream_rows(200, (64, 64), image_position=10000)
+    assert kv == 200 + 1 + 4096 and gs[0] == 200 and gs[-1] == kv - 1
+    i, j = np.divmod(np.arange(4096), 64)
+    assert np.array_equal(gp[1:], np.stack([np.full(4096, 10000), 10000 + i, 10000 + j], 1))
+
+
+def test_hidream_rows_validate():
+    L = oa.load()
+    assert L.omni_hidream_rows(0, 2, 2, 4096, None, None, None, None, None) == oa.EINVAL
+    assert L.omni_hidream_rows(3, 0, 2, 4096, None, None, None, None, None) == oa.EINVAL
+    assert L.omni_hidream_rows(3, 2, 2, -1, None, None, None, None, None) == oa.EINVAL
+    assert L.omni_hidream_rows(3, 2, 2, 4096, None, None, None, None, None) == oa.OK
