@@ -121,9 +121,10 @@ def run_dense_ws(c, kv_len=None):
 
 
 @pytest.mark.parametrize("hq,hk,q_len,kv_len,causal,batch", [
-    (8, 2, 256, 256, 0, 1),     # 16 tiles: every tile split into 32 chunks of a 4-tile key range (most empty)
+    # (with 256-row tiles, 128-key tiles and 256 resident workgroups on MI355X)
+    (8, 2, 256, 256, 0, 1),     # 8 items, each split into 32 chunks of a 2-tile key range (most chunks empty)
     (32, 8, 300, 700, 1, 2),    # causal: chunk ranges differ per tile
-    (32, 8, 1000, 1000, 0, 1),  # 256 tiles: every tile split in two
+    (32, 8, 1000, 1000, 0, 1),  # 128 items: each split in two
     (4, 4, 1, 1, 0, 1),
 ])
 def test_dit_tail_split_parity(oracle, hq, hk, q_len, kv_len, causal, batch):
