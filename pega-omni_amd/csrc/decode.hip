@@ -140,13 +140,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
       return pg[min(tb + 4 * i + r, t1 - 1) >> shift];
   };
   constexpr int kStride = kDecodeWaves * kTileKeys;
-  int pid[8] = {};
-  const int tb0 = t0 + wave * kTileKeys;
-  if (tb0 < t1) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pid[i] = page_of(tb0, i);
-  }
-  for (int tb = tb0; tb < t1; tb += kStride) {
+  // G = 1: two register tiles, the next tile's loads (and the page ids of the
+  // one after) issued before this tile's math. The tile after the split's
+  // last is loaded too, its keys clamped to slot t1 - 1 (cached), so every
+  // wait is a plain in-order count.
+  struct KVTile {
+    uint4 kr[8], vr[8];
+  };
+  auto load_tile = [&](KVTile& x, int tb, const int* pid) __attribute__((always_inline)) {
     int64_t off[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -156,21 +157,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
       else
         off[i] = (((int64_t)pid[i] << shift) | (t & pmask)) * per_slot;
     }
-    uint4 kr[8], vr[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = ldg16_stream(kb + off[i]);
+    for (int i = 0; i < 8; ++i) x.kr[i] = ldg16_stream(kb + off[i]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = ldg16_stream(vb + off[i]);
-    if (tb + kStride < t1) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + kStride, i);
-    }
-
+    for (int i = 0; i < 8; ++i) x.vr[i] = ldg16_stream(vb + off[i]);
+  };
+  auto compute_tile = [&](const KVTile& x, int tb) __attribute__((always_inline)) {
     float sc[G][8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float kf[8];
-      widen8(kr[i], kf);
+      widen8(x.kr[i], kf);
       const bool valid = tb + 4 * i + r < t1;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -204,11 +201,50 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float vf[8];
-      widen8(vr[i], vf);
+      widen8(x.vr[i], vf);
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(sc[g][i], vf[e], acc[g][e]);
+    }
+  };
+  const int tb0 = t0 + wave * kTileKeys;
+  if (G > 1 && tb0 < t1) {
+    // One tile at a time (G > 1: twice the math per tile, and the second
+    // register tile would cost more occupancy than it hides).
+    int pid[8] = {};
+    KVTile ta;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pid[i] = page_of(tb0, i);
+    for (int tb = tb0; tb < t1; tb += kStride) {
+      load_tile(ta, tb, pid);
+      if (tb + kStride < t1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + kStride, i);
+      }
+      compute_tile(ta, tb);
+    }
+  } else if (tb0 < t1) {
+    int pid[8] = {};
+    KVTile ta, tn;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pid[i] = page_of(tb0, i);
+    load_tile(ta, tb0, pid);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pid[i] = page_of(tb0 + kStride, i);
+    for (int tb = tb0;; tb += 2 * kStride) {
+      load_tile(tn, tb + kStride, pid);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + 2 * kStride, i);
+      __builtin_amdgcn_sched_barrier(0);  // keep the next tile's loads ahead of this tile's math
+      compute_tile(ta, tb);
+      if (tb + kStride >= t1) break;
+      load_tile(ta, tb + 2 * kStride, pid);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + 3 * kStride, i);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_tile(tn, tb + kStride);
+      if (tb + 2 * kStride >= t1) break;
     }
   }
 
