@@ -187,7 +187,9 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
  * q rows at q + n * q_stride + h * 128 (h < hq = G * hk), k and v [slots][hk][128],
  * out [q_len][hq][128]; row n sees the first *kv_len_at keys, with causal
  * only keys 0..n. The reference fixes G = 4 and hk = gridDim.y; here hq and hk
- * are arguments (G in {1,2,4,8}). */
+ * are arguments (G in {1,2,4,8}). When the last round of tiles would fill at
+ * most half the GPU, its tiles run as two workgroups of half the rows each
+ * (no workspace; each row is computed the same way). */
 int omni_hidream_attend(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
                         int q_stride, int causal, float scale_log2, int hq, int hk, void* stream);
 
@@ -238,9 +240,10 @@ int omni_hidream_qk_rope(void* qkv, int ld, const void* q_norm, const void* k_no
 /* The batched call with a workspace: the last fraction of a round of tiles
  * (tiles % resident workgroups) is split by keys into chunks that fill the
  * round, and a combine kernel merges the chunks (log-sum-exp). Same results
- * to rounding; workspace NULL runs unsplit. workspace_bytes must be at least
- * omni_hidream_workspace_bytes() (16-byte aligned); the split depends only on
- * the shape and the device, never on *kv_len_at. */
+ * to rounding; workspace NULL runs as omni_hidream_attend_batched.
+ * workspace_bytes must be at least omni_hidream_workspace_bytes() (16-byte
+ * aligned); the split depends only on the shape and the device, never on
+ * *kv_len_at. */
 int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
                            int q_stride, int causal, float scale_log2, int hq, int hk, int batch, int64_t q_bstride,
                            int64_t kv_bstride, int64_t out_bstride, void* workspace, int64_t workspace_bytes,

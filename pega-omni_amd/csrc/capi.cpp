@@ -341,6 +341,18 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
   return ok();
 }
 
+namespace {
+
+// Workgroups of the tiled kernel resident at once on the current device (one per CU).
+int resident_tiled_groups() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return cus;
+}
+
+}  // namespace
+
 int omni_hidream_attend_batched(const void* q, const void* k, const void* v, void* out, int q_len,
                                 const int32_t* kv_len_at, int q_stride, int causal, float scale_log2, int hq, int hk,
                                 int batch, int64_t q_bstride, int64_t kv_bstride, int64_t out_bstride, void* stream) {
@@ -370,24 +382,13 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
   a.hq = hq;
   a.hk = hk;
   a.scale_log2 = scale_log2;
+  a.halved = omni::dit_halves(a, batch, resident_tiled_groups());
   const int rc = omni::launch_dit(a, batch, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: shape not implemented");
   if (rc != 0)
     return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
 }
-
-namespace {
-
-// Workgroups of the tiled kernel resident at once on the current device (one per CU).
-int resident_tiled_groups() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  return cus;
-}
-
-}  // namespace
 
 int64_t omni_hidream_workspace_bytes(void) { return (int64_t)resident_tiled_groups() * omni::kSegmentBytes; }
 

@@ -72,6 +72,9 @@ struct TiledArgs {
   // chunk: O[128 rows][128] then (m, l)[128 rows]); 0 chunks = no split.
   int split_from, split_k;
   float* ws;
+  // Row halves (dense, no split): the last `halved` items run as two
+  // workgroups of kTiledRows / 2 packed rows each; 0 = none.
+  int halved;
 };
 
 // Packed (position, head) query rows per MFMA tile: one 8-wave workgroup, one per CU.
@@ -124,5 +127,7 @@ int launch_rope(const RopeArgs& a, int mode, hipStream_t stream);
 int launch_dit(const TiledArgs& a, int batch, hipStream_t stream);
 // Items and the tail split launch_dit would use for a call (split_k = 0: none).
 void dit_split(const TiledArgs& a, int batch, int resident, int* items, int* split_from, int* split_k);
+// Items launch_dit should run as row halves when no split is used (0: none).
+int dit_halves(const TiledArgs& a, int batch, int resident);
 
 }  // namespace omni

@@ -125,7 +125,7 @@ struct Tile {
   int64_t per_slot;          // paged: elements per slot
 };
 
-template <int G, bool PAGED>
+template <int G, bool PAGED, bool HALVES = false>
 __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items, int ntiles) {
   // DiT, XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
   // contiguous block of work items so the tiles sharing one K/V head (and
@@ -137,8 +137,28 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   // DiT tail split: the first split_from items run whole, then every later
   // item runs as split_k key chunks (workgroups dispatched after all whole
   // items, so they fill the last round), each with its own XCD-aware order.
-  int idx, chunk = -1;
-  if (!PAGED && a.split_k > 0) {
+  // DiT row halves (HALVES): the last `halved` items run as two workgroups
+  // of kBM / 2 packed rows, in the same order as the split chunks; waves
+  // 0..3 (one per SIMD) compute the first half, waves 4..7 the second, and
+  // all eight load the K/V tiles.
+  int idx, chunk = -1, half = -1;
+  if constexpr (HALVES) {
+    const int halves_from = items - a.halved;
+    const int whole8 = ((halves_from + 7) >> 3) << 3;
+    if ((int)blockIdx.x < whole8) {
+      const int per = whole8 >> 3;
+      idx = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+      if (idx >= halves_from) return;
+    } else {
+      const int b2 = blockIdx.x - whole8;
+      const int units = a.halved * 2;
+      const int per = (units + 7) >> 3;
+      const int u = (b2 & 7) * per + (b2 >> 3);
+      if (u >= units) return;
+      idx = halves_from + (u >> 1);
+      half = u & 1;
+    }
+  } else if (!PAGED && a.split_k > 0) {
     const int whole8 = ((a.split_from + 7) >> 3) << 3;
     if ((int)blockIdx.x < whole8) {
       const int per = whole8 >> 3;
@@ -188,7 +208,10 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     t.q = a.q + b * a.q_bstride + (int64_t)q0 * a.q_stride;
     t.out = a.out + b * a.out_bstride + (int64_t)q0 * a.hq * kHead;
     t.len = *a.kv_len_at;
-    t.last = a.causal ? min(t.len, q0 + t.nq) : t.len;
+    // A half's rows end at position (kBM / 2) (half + 1) / G of the tile.
+    const int np = half < 0 ? t.nq : min(t.nq, (kBM / 2) * (half + 1) / G);
+    if (half > 0 && (kBM / 2) * half / G >= t.nq) return;  // a second half with no rows
+    t.last = a.causal ? min(t.len, q0 + np) : t.len;
     t.qpos0 = q0;
     t.kv_stride = (int64_t)a.hk * kHead;
     t.kbase = a.k + b * a.kv_bstride + (int64_t)kvh * kHead;
@@ -206,7 +229,10 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   // This lane's query column: packed row r = 32 wave + j.
   const int r = wave * 32 + j;
   const int p = r / G, head = kvh * G + r % G;
-  const bool row_ok = p < t.nq;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // Waves outside this workgroup's half only load K/V tiles (wave-uniform).
+  const bool active = half < 0 || (wave_u >> 2) == half;
+  const bool row_ok = p < t.nq && active;
   int lim;  // keys this row sees
   if constexpr (PAGED)
     lim = row_ok ? t.pos[p] + 1 : 0;
@@ -232,7 +258,6 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   // rows per load; lane l takes row kRowsPerWave w + 4 i + l / 16 and LDS
   // slot l % 16.
   // Keys past `last` repeat the last key (their scores are masked).
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   // Dense sources: within a full tile a lane's rows and chunks are fixed, so
   // its element offsets from the tile's first key are constants (32-bit) and a
   // tile adds one uniform base: loads take a scalar base and a vector offset.
@@ -450,6 +475,19 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
     __syncthreads();
   };
+  // A wave outside the half: the same loads and barriers, no compute.
+  auto load_step = [&](int st, bf16_t* nxt) {
+    if (st + 1 < s_hi) issue_tile((st + 1) * kBN, nxt);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  };
+  if (HALVES && !active) {
+    for (int st = s_lo; st < s_hi; st += 2) {
+      load_step(st, smem1);
+      if (st + 1 < s_hi) load_step(st + 1, smem0);
+    }
+    return;
+  }
   for (int st = s_lo; st < s_hi; st += 2) {
     tile_step(st, smem0, smem1);
     if (st + 1 < s_hi) tile_step(st + 1, smem1, smem0);
@@ -534,10 +572,15 @@ int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) 
   int grid = ((items + 7) >> 3) << 3;
   if (!PAGED && a.split_k > 0)
     grid = (((a.split_from + 7) >> 3) << 3) + ((((items - a.split_from) * a.split_k + 7) >> 3) << 3);
+  const bool halves = !PAGED && a.split_k == 0 && a.halved > 0;
+  if (halves) grid = (((items - a.halved + 7) >> 3) << 3) + (((a.halved * 2 + 7) >> 3) << 3);
   switch (a.hq / a.hk) {
 #define OMNI_CASE(G)                                                                       \
   case G:                                                                                  \
-    tiled_attn<G, PAGED><<<grid, kThreads, 0, stream>>>(a, items, ntiles);       \
+    if (halves)                                                                            \
+      tiled_attn<G, false, true><<<grid, kThreads, 0, stream>>>(a, items, ntiles);         \
+    else                                                                                   \
+      tiled_attn<G, PAGED><<<grid, kThreads, 0, stream>>>(a, items, ntiles);               \
     break;
     OMNI_CASE(1)
     OMNI_CASE(2)
@@ -564,7 +607,20 @@ int launch_dit(const TiledArgs& a, int batch, hipStream_t stream) {
   const int ntiles = (a.q_len + kBM / G - 1) / (kBM / G);
   const long long items = (long long)ntiles * a.hk * batch;
   if (items > (1LL << 30)) return -2;
+  if (a.halved < 0 || a.halved > items || a.halved > (1 << 29)) return -2;
   return launch_tiled<false>(a, (int)items, ntiles, stream);
+}
+
+// Without a workspace: when the last round holds at most half the resident
+// workgroups, its items run as row halves (two workgroups each), so that
+// round takes about half a tile's time on the four SIMDs of each CU.
+int dit_halves(const TiledArgs& a, int batch, int resident) {
+  const int G = a.hq / a.hk;
+  const int ntiles = (a.q_len + kBM / G - 1) / (kBM / G);
+  const long long n = (long long)ntiles * a.hk * batch;
+  if (resident <= 0 || n <= 0 || n > (1LL << 30)) return 0;
+  const int rem = (int)(n % resident);
+  return 2 * rem > resident ? 0 : rem;
 }
 
 // With `resident` workgroups in flight (one per CU), items - items % resident

@@ -73,9 +73,13 @@ def oracle_dense(oracle, c, b=0, kv_len=None):
                                c.causal, c.scale_log2, nthreads=16)
 
 
+# On a 256-CU GPU the workspace-free call runs the last round's items as row
+# halves when they fill at most half of it: every case below but the
+# 1100-query one (144 items, all whole) runs as halves only. (16, 8, 65) and
+# (4, 4, 1) have second halves with one and no rows.
 @pytest.mark.parametrize("hq,hk,q_len,kv_len,causal", [
     (32, 8, 300, 300, 1), (32, 8, 257, 333, 0), (8, 8, 100, 130, 0), (4, 4, 1, 1, 0), (16, 8, 65, 64, 1),
-    (32, 4, 40, 500, 0),
+    (32, 4, 40, 500, 0), (32, 8, 1100, 300, 1),
 ])
 def test_dit_parity(oracle, hq, hk, q_len, kv_len, causal):
     c = W.dense_case(hq, hk, q_len, kv_len, causal, seed=q_len)
@@ -135,9 +139,10 @@ def test_dit_tail_split_parity(oracle, hq, hk, q_len, kv_len, causal, batch):
 
 
 def test_dit_tail_split_config5_matches_unsplit(oracle):
-    """Config 5 (2176 tiles: 2048 whole, 128 split into 4 chunks on a 256-CU
-    GPU) agrees with the unsplit kernel everywhere and with the oracle on the
-    last 128 query positions (all in split tiles)."""
+    """Config 5 (1088 tiles: 1024 whole, 64 split into 4 chunks on a 256-CU
+    GPU) agrees with the workspace-free call (there the 64 run as row halves)
+    everywhere and with the oracle on the last 128 query positions (all in
+    split tiles)."""
     c = W.dense_case(32, 8, 4352, 4352, 0, batch=2, seed=5000)
     got, ref = run_dense_ws(c), run_dense(c)
     for b in range(2):
@@ -148,6 +153,22 @@ def test_dit_tail_split_config5_matches_unsplit(oracle):
                                nthreads=16)
     assert_close(got[1, -128:], tail, what="config5 split tail vs oracle")
     del sub
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_dit_row_halves_match_split(oracle, causal):
+    """544 items: on a 256-CU GPU the last 32 (kv head 7, queries 2304..)
+    run as row halves without a workspace and as 8 key chunks with one. Both
+    agree with each other everywhere and with the oracle on the last 128
+    queries (whole tiles for heads 0..27, halves for 28..31)."""
+    c = W.dense_case(32, 8, 4352, 1024, causal, seed=31 + causal)
+    got, split = run_dense(c)[0], run_dense_ws(c)[0]
+    assert_close(got, split, what="halves vs split")
+    # Queries 4224.. see all 1024 keys, causal or not.
+    want = oracle.dense_attend(np.ascontiguousarray(c.q[0, -128:]), np.ascontiguousarray(c.k[0]),
+                               np.ascontiguousarray(c.v[0]), 128, 1024, c.q_stride, 32, 8, 0, c.scale_log2,
+                               nthreads=16)
+    assert_close(got[-128:], want, what=f"halves tail vs oracle c{causal}")
 
 
 @pytest.mark.parametrize("page", [1, 2, 4, 8, 64])
