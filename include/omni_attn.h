@@ -166,10 +166,11 @@ typedef struct omni_attn_prefill_plan {
 /* Host: validate (seq_h, pos_h) for `rows` ragged rows and write the work list
  * into work_h (capacity work_cap int32): a header of 16 int32 whose entries
  * 0..8 bound the item ranges of the GPU's 8 XCDs, then 4 int32 per (tile, kv
- * head) item (sequence, first row, rows, kv head). Items run sequence by
- * sequence, each kv head's tiles longest first, so the workgroups on one XCD
- * share one sequence's K/V in that XCD's L2; the XCD ranges have nearly equal
- * rows x keys. Returns OMNI_ATTN_EWORKSPACE with plan->work_bytes set when
+ * head) item (sequence, first row, rows, kv head). Workgroup i runs item
+ * header[i % 8] + i / 8. In workgroup order the tiles run by the keys they
+ * see, most first, each with its hk kv heads, so every XCD ends on short
+ * tiles and always sees the same kv heads (their K/V stays in its L2); the
+ * XCD ranges differ by at most one item. Returns OMNI_ATTN_EWORKSPACE with plan->work_bytes set when
  * work_h is too small. */
 int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_t* seq_h, const int32_t* pos_h,
                                 int32_t* work_h, int64_t work_cap, omni_attn_prefill_plan* plan);

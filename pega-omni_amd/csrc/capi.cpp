@@ -9,7 +9,6 @@
 #include <new>
 #include <array>
 #include <climits>
-#include <unordered_map>
 #include <vector>
 #include <cmath>
 #include <cstdarg>
@@ -261,50 +260,31 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   plan->reserved = 0;
   if (!work_h || need > work_cap)
     return fail(OMNI_ATTN_EWORKSPACE, "prefill_plan: work list needs %lld int32", (long long)need);
-  // Item order: sequences by their longest tile, then per sequence each kv
-  // head's tiles, longest first. The workgroups resident on one XCD then work
-  // on one (sequence, kv head) at a time and share its K/V in that XCD's L2,
-  // and each XCD ends on short tiles.
-  std::unordered_map<int32_t, int32_t> longest;
-  for (const auto& t : tl) {
-    auto it = longest.find(t[0]);
-    if (it == longest.end() || it->second < t[3]) longest[t[0]] = t[3];
-  }
-  std::stable_sort(tl.begin(), tl.end(), [&](const auto& x, const auto& y) {
-    const int32_t lx = longest[x[0]], ly = longest[y[0]];
-    if (lx != ly) return lx > ly;
+  // Item order: tiles by the keys they see, most first (a tile's time grows
+  // with its key tiles, whatever its row count), each followed by its hk kv
+  // heads. Workgroup i runs on XCD i % 8 and item k goes to XCD k % 8, so each
+  // XCD's workgroups run longest first and the grid ends on short tiles; and
+  // as hk is a power of two, an XCD always sees the same kv heads (h = x mod
+  // hk for hk <= 8, h = x mod 8 beyond), so its L2 holds their K/V.
+  std::stable_sort(tl.begin(), tl.end(), [](const auto& x, const auto& y) {
+    if (x[3] != y[3]) return x[3] > y[3];
     if (x[0] != y[0]) return x[0] < y[0];
-    return x[3] > y[3];
+    return x[1] < y[1];
   });
-  int32_t* it = work_h + omni::kPrefillWorkHeader;
-  std::vector<double> cost;
-  cost.reserve(items);
-  for (int64_t b = 0; b < tiles;) {
-    int64_t e = b + 1;
-    while (e < tiles && tl[e][0] == tl[b][0]) ++e;
-    for (int h = 0; h < hk; ++h)
-      for (int64_t i = b; i < e; ++i) {
-        it[0] = tl[i][0];
-        it[1] = tl[i][1];
-        it[2] = tl[i][2];
-        it[3] = h;
-        it += 4;
-        cost.push_back((double)tl[i][2] * tl[i][3]);  // rows x keys of the tile
-      }
-    b = e;
-  }
-  // The 8 XCDs (workgroup i runs on XCD i % 8) take contiguous ranges of
-  // nearly equal cost.
-  double total = 0;
-  for (double c : cost) total += c;
   int32_t* hdr = work_h;
   for (int k = 0; k < omni::kPrefillWorkHeader; ++k) hdr[k] = 0;
-  double run = 0;
-  int64_t i = 0;
-  for (int x = 1; x < omni::kXcds; ++x) {
-    const double target = total * x / omni::kXcds;
-    while (i < items && run + 0.5 * cost[i] < target) run += cost[i++];
-    hdr[x] = (int32_t)i;
+  int32_t* body = work_h + omni::kPrefillWorkHeader;
+  int64_t at = 0;
+  for (int x = 0; x < omni::kXcds; ++x) {
+    hdr[x] = (int32_t)at;
+    for (int64_t k = x; k < items; k += omni::kXcds, ++at) {
+      const auto& t = tl[k / hk];
+      int32_t* it = body + 4 * at;
+      it[0] = t[0];
+      it[1] = t[1];
+      it[2] = t[2];
+      it[3] = (int32_t)(k % hk);
+    }
   }
   hdr[omni::kXcds] = (int32_t)items;
   int32_t widest = 0;

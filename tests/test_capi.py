@@ -152,38 +152,49 @@ def test_prefill_plan_items_cover_every_row_and_head_once():
     assert plan.workgroups == 8 * int(np.diff(hdr[:9]).max())
 
 
-def test_prefill_plan_groups_sequence_and_kv_head():
-    r = W.ragged_prefill_case(6, 16, 4, 40, 400, 0, 200, seed=5)
-    plan, hdr, items = _plan_host(r.rows, 16, 4, r.seq, r.pos)
-    keys = np.array([r.pos[f + n - 1] + 1 for _, f, n, _ in items])
-    # each (sequence, kv head) is one contiguous run, longest tile first
-    runs = [(int(s), int(h)) for s, _, _, h in items]
-    starts = [i for i in range(len(runs)) if i == 0 or runs[i] != runs[i - 1]]
-    assert len(starts) == len(set(runs)), "a (sequence, kv head) group is split"
-    for a, b in zip(starts, starts[1:] + [len(runs)]):
-        assert np.all(np.diff(keys[a:b]) <= 0)
-    # sequences by their longest tile, descending; kv heads in order within one
-    seqs = [runs[a][0] for a in starts]
-    longest = {s: keys[items[:, 0] == s].max() for s in set(seqs)}
-    order = list(dict.fromkeys(seqs))
-    assert all(longest[x] >= longest[y] for x, y in zip(order, order[1:]))
-    for s in order:
-        assert [runs[a][1] for a in starts if runs[a][0] == s] == list(range(4))
-    # the 8 XCD ranges carry nearly equal rows x keys (within the largest item)
-    cost = items[:, 2].astype(float) * keys
-    per = [cost[hdr[x]:hdr[x + 1]].sum() for x in range(8)]
-    assert max(per) - min(per) <= 2 * cost.max() + 1e-9
+def _dispatch_order(hdr, items):
+    """Items in the order workgroups are numbered: workgroup i runs item
+    hdr[i % 8] + i // 8 (XCD i % 8); holes where an XCD's range is exhausted."""
+    out = []
+    for i in range(8 * int(np.diff(hdr[:9]).max())):
+        x, j = i % 8, i // 8
+        if hdr[x] + j < hdr[x + 1]:
+            out.append(items[hdr[x] + j])
+    return np.array(out)
+
+
+@pytest.mark.parametrize("hk", [1, 2, 4, 8, 16])
+def test_prefill_plan_runs_longest_first_and_pins_kv_heads(hk):
+    r = W.ragged_prefill_case(6, 4 * hk, hk, 40, 400, 0, 200, seed=5)
+    plan, hdr, items = _plan_host(r.rows, 4 * hk, hk, r.seq, r.pos)
+    keys = lambda it: np.array([r.pos[f + n - 1] + 1 for _, f, n, _ in it])
+    # In workgroup order: tiles by keys, most first, each with its hk kv heads in order.
+    order = _dispatch_order(hdr, items)
+    assert len(order) == len(items)
+    assert np.all(np.diff(keys(order)) <= 0)
+    tiles = order.reshape(-1, hk, 4)
+    assert np.all(tiles[:, :, 3] == np.arange(hk)) and np.all(tiles[:, :, :3] == tiles[:, :1, :3])
+    # Every XCD runs longest first and always sees the same kv heads.
+    for x in range(8):
+        mine = items[hdr[x]:hdr[x + 1]]
+        assert np.all(np.diff(keys(mine)) <= 0)
+        assert set(int(h) % 8 for h in mine[:, 3]) <= {x % hk if hk <= 8 else x}
+    # The XCD ranges differ by at most one item.
+    sizes = np.diff(hdr[:9])
+    assert sizes.max() - sizes.min() <= 1 and plan.workgroups == 8 * int(sizes.max())
 
 
 def test_prefill_plan_breaks_runs_at_position_gaps():
     seq = np.array([0, 0, 0, 1, 1, 0, 0], np.int32)
     pos = np.array([5, 6, 8, 0, 1, 9, 10], np.int32)
-    plan, _, items = _plan_host(7, 4, 4, seq, pos)
+    plan, hdr, items = _plan_host(7, 4, 4, seq, pos)
     assert plan.tiles == 4
-    # sequence 0's tiles (both of its runs) for kv head 0, longest first, then sequence 1
-    assert _tiles(pos, items) == [(0, 5, 2, 11), (0, 2, 1, 9), (0, 0, 2, 7), (1, 3, 2, 2)]
-    assert [tuple(w) for w in items[:3]] == [(0, 5, 2, 0), (0, 2, 1, 0), (0, 0, 2, 0)]
-    assert [int(h) for h in items[:12, 3]] == [0] * 3 + [1] * 3 + [2] * 3 + [3] * 3
+    # tiles by keys, most first: both runs of sequence 0, then sequence 1
+    order = _dispatch_order(hdr, items)
+    assert _tiles(pos, order) == [(0, 5, 2, 11), (0, 2, 1, 9), (0, 0, 2, 7), (1, 3, 2, 2)]
+    assert [tuple(w) for w in order[:5]] == [(0, 5, 2, 0), (0, 5, 2, 1), (0, 5, 2, 2), (0, 5, 2, 3), (0, 2, 1, 0)]
+    # XCD 0 takes items 0 and 8: kv head 0 of the first and third tiles
+    assert [tuple(w) for w in items[hdr[0]:hdr[1]]] == [(0, 5, 2, 0), (0, 0, 2, 0)]
 
 
 def test_rope_entry_points_validate_before_launch():
