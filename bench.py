@@ -547,6 +547,8 @@ def main():
         log(f"[bench] {extra['config5']}")
         if args.only == 0:
             extra["config5_mha"] = dit_bench(stream, args.steps, args.warmup, hk=32)
+            # the reference's signature (no workspace): the last round's tiles run as row halves
+            extra["config5_no_workspace"] = dit_bench(stream, args.steps, args.warmup, split=False)
         if args.only == 5:  # A/B of the tail split, alternating
             for i in range(2):
                 extra[f"config5_unsplit_{i}"] = dit_bench(stream, args.steps, args.warmup, split=False)
