@@ -612,8 +612,9 @@ int launch_dit(const TiledArgs& a, int batch, hipStream_t stream) {
 }
 
 // Without a workspace: when the last round holds at most half the resident
-// workgroups, its items run as row halves (two workgroups each), so that
-// round takes about half a tile's time on the four SIMDs of each CU.
+// workgroups, its items run as row halves (two workgroups each, on twice the
+// CUs); with one computing wave per SIMD such a round takes about 0.7 of a
+// full round's time.
 int dit_halves(const TiledArgs& a, int batch, int resident) {
   const int G = a.hq / a.hk;
   const int ntiles = (a.q_len + kBM / G - 1) / (kBM / G);
