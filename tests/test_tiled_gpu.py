@@ -214,3 +214,23 @@ def test_dit_reads_no_key_past_kv_len(oracle, causal):
     oa.hidream_attend(q, k, v, out, c.q_len, kvl, c.q_stride, causal, c.scale_log2, c.hq, c.hk)
     torch.cuda.synchronize()
     assert_close(host_bits(out), oracle_dense(oracle, c, kv_len=259), what=f"kv_len 259 with NaN past it, c{causal}")
+
+
+@pytest.mark.parametrize("layout", ["gaps", "interleaved"])
+def test_prefill_runs_split_at_gaps_and_interleaving(oracle, layout):
+    """Rows whose positions jump inside a sequence, or whose sequences
+    alternate row by row: the plan cuts them into separate runs (single rows
+    when interleaved), and each row still sees keys 0..pos of its sequence."""
+    base = W.ragged_prefill_case(3, 32, 8, 150, 300, 20, 200, seed=77)
+    rng = np.random.default_rng(78)
+    if layout == "gaps":
+        keep = np.sort(rng.choice(base.rows, size=base.rows * 2 // 3, replace=False))  # drop a third of the rows
+    else:
+        per_seq = [np.flatnonzero(base.seq == s) for s in range(3)]
+        n = min(len(x) for x in per_seq)
+        keep = np.stack([x[:n] for x in per_seq], axis=1).reshape(-1)  # seq 0, 1, 2, 0, 1, 2, ...
+    c = W.PagedCase(hq=32, hk=8, page=base.page, pos=base.pos[keep], seq=base.seq[keep], ragged=1,
+                    indptr=base.indptr, pages=base.pages, num_pages=base.num_pages, qkv=base.qkv[keep], kv=base.kv)
+    pf = oa.prefill_plan(c.rows, 32, 8, c.page, c.seq, c.pos)
+    assert pf.plan.tiles > (c.rows + 63) // 64  # really cut into more, shorter runs
+    assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill {layout}")
