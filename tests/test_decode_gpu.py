@@ -178,3 +178,11 @@ def test_reads_no_slot_past_the_keys(oracle, chunk):
     c.kv = c.kv.copy()
     c.kv[~seen] = 0x7FC0  # bf16 NaN
     assert_close(DevPaged(c).decode(chunk=chunk), oracle_out(oracle, c), what=f"NaN past the keys chunk={chunk}")
+
+
+@pytest.mark.parametrize("chunk", [0, 1024])
+def test_long_contexts(oracle, chunk):
+    """Rows of 20k-64k keys: many splits per row (the plan's chunk, or 1024),
+    far past the configs' 3000-key bound."""
+    c = W.paged_decode_case(3, 8, 2, 20000, 65536, seed=15)  # 8q/2kv: a 1 KiB slot keeps the pool small
+    assert_close(DevPaged(c).decode(chunk=chunk), oracle_out(oracle, c), what=f"long contexts chunk {chunk}")

@@ -234,3 +234,14 @@ def test_prefill_runs_split_at_gaps_and_interleaving(oracle, layout):
     pf = oa.prefill_plan(c.rows, 32, 8, c.page, c.seq, c.pos)
     assert pf.plan.tiles > (c.rows + 63) // 64  # really cut into more, shorter runs
     assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill {layout}")
+
+
+def test_prefill_long_sequence(oracle):
+    """One sequence of 6000 new rows over 3000 cached keys: 94 tiles per kv
+    head. The oracle checks the first and last 96 rows (rows are independent)."""
+    c = W.ragged_prefill_case(1, 32, 8, 6000, 6000, 3000, 3000, seed=79)
+    got = run_prefill(c)
+    pick = np.r_[0:96, c.rows - 96:c.rows]
+    sub = W.PagedCase(hq=32, hk=8, page=c.page, pos=c.pos[pick], seq=c.seq[pick], ragged=1, indptr=c.indptr,
+                      pages=c.pages, num_pages=c.num_pages, qkv=c.qkv[pick], kv=c.kv)
+    assert_close(got[pick], oracle_paged(oracle, sub), what="long prefill, first and last rows")
