@@ -194,24 +194,109 @@ def cpu_decode_baseline(cfg=3, rows=32, min_seconds=10.0, threads=None):
     c.pages = rng.permutation(used).astype(np.int32)
     c.num_pages = used
 
-    def values(n):  # normal bf16 in +-[1/8, 2) with random sign and mantissa: timing only
-        return (rng.integers(0, 1 << 16, n, dtype=np.uint16) & np.uint16(0x81FF)) | np.uint16(0x3E00)
-
-    c.qkv = values(rows * (c.hq + 2 * c.hk) * 128).reshape(rows, -1)
-    c.kv = values(used * c.page * 2 * c.hk * 128).reshape(used * c.page, -1)
+    c.qkv = _timing_values(rng, rows * (c.hq + 2 * c.hk) * 128).reshape(rows, -1)
+    c.kv = _timing_values(rng, used * c.page * 2 * c.hk * 128).reshape(used * c.page, -1)
     args = (c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, c.page, c.hq, c.hk, c.scale)
-    oracle.paged_attend(*args, context=c.context, nthreads=threads)  # warm
+    sec, reps, el = _repeat(lambda: oracle.paged_attend(*args, context=c.context, nthreads=threads), min_seconds)
+    which = "all" if rows == W.CONFIGS[cfg]["rows"] else f"first {rows} of"
+    text = (f"config{cfg}: {which} {W.CONFIGS[cfg]['rows']} sessions of one layer, pages compacted to a "
+            f"{used}-page pool "
+            f"({c.kv_bytes() / 1e9:.3f} GB algorithmic), {reps} reps over {el:.1f} s")
+    return c.kv_bytes() / sec / 1e9, sec, threads, text
+
+
+def _timing_values(rng, n):
+    """Normal bf16 bit patterns in +-[1/8, 2) with random sign and mantissa:
+    inputs for CPU timing only (their outputs are not checked)."""
+    import numpy as np
+
+    return (rng.integers(0, 1 << 16, n, dtype=np.uint16) & np.uint16(0x81FF)) | np.uint16(0x3E00)
+
+
+def _repeat(fn, min_seconds):
+    fn()  # warm
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.paged_attend(*args, context=c.context, nthreads=threads)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
         if el >= min_seconds:
-            break
-    sec = el / reps
-    text = (f"config{cfg}: first {rows} of {W.CONFIGS[cfg]['rows']} sessions of one layer "
-            f"({c.kv_bytes() / 1e9:.3f} GB algorithmic), {reps} reps over {el:.1f} s")
-    return c.kv_bytes() / sec / 1e9, sec, threads, text
+            return el / reps, reps, el
+
+
+def cpu_prefill_baseline(rows=96, min_seconds=3.0, threads=None):
+    """The oracle on a bounded sample of config 4: `rows` seeded random rows
+    of the B = 8 draw (each with its own causal key count, over its
+    sequence's paged keys). GFLOP/s at 4 * 128 flops per (q head, query, key)."""
+    import numpy as np
+
+    import oracle
+    import workloads as W
+
+    threads = threads or min(16, os.cpu_count() or 1)
+    c = W.config_case(4, values=None)
+    rng = np.random.default_rng(44)
+    idx = np.sort(rng.choice(c.rows, rows, replace=False))
+    pos, seq = c.pos[idx].copy(), c.seq[idx].copy()
+    qkv = _timing_values(rng, rows * (c.hq + 2 * c.hk) * 128).reshape(rows, -1)
+    kv = _timing_values(rng, c.num_pages * c.page * 2 * c.hk * 128).reshape(c.num_pages * c.page, -1)
+    sec, reps, el = _repeat(lambda: oracle.paged_attend(qkv, kv, pos, seq, 1, c.indptr, c.pages, c.page, c.hq, c.hk,
+                                                        c.scale, nthreads=threads), min_seconds)
+    fl = int(4 * 128 * c.hq * (pos.astype(np.int64) + 1).sum())
+    return dict(value=round(fl / sec / 1e9, 3), unit="GFLOP/s", cores=threads, kind="port",
+                sample=f"config4: {rows} seeded random rows of the {c.rows}-row draw ({fl / 1e9:.2f} GFLOP), "
+                       f"{reps} reps over {el:.1f} s", seconds_per_sample=round(sec, 4))
+
+
+def cpu_dit_baseline(q_rows=48, min_seconds=3.0, threads=None):
+    """The oracle on a bounded sample of config 5: the first `q_rows` query
+    positions (all 32 heads) of one CFG half over all 4352 keys."""
+    import numpy as np
+
+    import oracle
+    import workloads as W
+
+    threads = threads or min(16, os.cpu_count() or 1)
+    cfg = W.CONFIGS[5]
+    hq, hk, kv_len = cfg["hq"], cfg["hk"], cfg["kv_len"]
+    rng = np.random.default_rng(55)
+    q_stride = (hq + 2 * hk) * 128
+    q = _timing_values(rng, q_rows * q_stride).reshape(q_rows, q_stride)
+    k = _timing_values(rng, kv_len * hk * 128).reshape(kv_len, -1)
+    v = _timing_values(rng, kv_len * hk * 128).reshape(kv_len, -1)
+    sl2 = (128 ** -0.5) * 1.4426950408889634
+    sec, reps, el = _repeat(lambda: oracle.dense_attend(q, k, v, q_rows, kv_len, q_stride, hq, hk, 0, sl2,
+                                                        nthreads=threads), min_seconds)
+    fl = 4 * 128 * hq * q_rows * kv_len
+    return dict(value=round(fl / sec / 1e9, 3), unit="GFLOP/s", cores=threads, kind="port",
+                sample=f"config5: the first {q_rows} of 4352 query positions of one CFG half, all {hq} heads, "
+                       f"over 4352 keys ({fl / 1e9:.2f} GFLOP), {reps} reps over {el:.1f} s",
+                seconds_per_sample=round(sec, 4))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baselines(head_cpu):
+    """The CPU path (the oracle, a C port of the reference math) on every
+    BASELINE config: config 1 in full, one config 2 layer, config 3's sample
+    (the headline's cpu_baseline), and bounded samples of configs 4 and 5."""
+    out = {"cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
+    for cfg, rows, secs in ((1, 4, 3.0), (2, 64, 3.0)):
+        v, sec, thr, text = cpu_decode_baseline(cfg, rows=rows, min_seconds=secs)
+        out[f"config{cfg}"] = dict(value=round(v, 3), unit="GB/s", cores=thr, kind="port", sample=text,
+                                   seconds_per_sample=round(sec, 4))
+    out["config3"] = head_cpu
+    out["config4"] = cpu_prefill_baseline()
+    out["config5"] = cpu_dit_baseline()
+    return out
 
 
 def prefill_bench(stream, steps, warmup):
@@ -481,6 +566,76 @@ def copy_calibration(mb):
     print(json.dumps({"copy_calibration_mib": mb, "bytes_read": mb << 20, "bytes_written": mb << 20}))
 
 
+def summarize_profile(dirs, kernels, last, flops=None, cus=256, xcds=8):
+    """Summarise rocprofv3 CSV output (one directory per pass) for the last
+    `last` dispatches of each kernel whose name contains one of `kernels`
+    (the timed calls of a bench.py run: its warmup calls come first). Prints a
+    markdown table: the mean kernel-trace duration of each kernel and of one
+    call (their sum), every counter of the first kernel averaged per dispatch,
+    and the derived figures. GRBM_GUI_ACTIVE counts on each of the `xcds` XCDs
+    and is summed over them; SQ_VALU_MFMA_BUSY_CYCLES is summed over the
+    cus x 4 SIMDs."""
+    import csv
+    import glob
+
+    durs = {k: [] for k in kernels}
+    counters = {}
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+            allrows = list(csv.DictReader(open(path)))
+            for k in kernels:
+                rows = sorted((r for r in allrows if k in r["Kernel_Name"]), key=lambda r: int(r["Start_Timestamp"]))
+                durs[k] += [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3 for r in rows[-last:]]
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            per = {}
+            for r in csv.DictReader(open(path)):
+                if kernels[0] in r["Kernel_Name"]:
+                    per.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+            for disp in sorted(per)[-last:]:
+                for name, v in per[disp].items():
+                    counters.setdefault(name, []).append(v)
+    avg = {k: sum(v) / len(v) for k, v in counters.items()}
+    lines = [f"| quantity | value (mean over the last {last} dispatches of each kernel per run) |", "|---|---|"]
+    call_us = 0.0
+    for k in kernels:
+        if durs[k]:
+            us = sum(durs[k]) / len(durs[k])
+            call_us += us
+            lines.append(f"| kernel-trace duration of `{k}` | {us:.2f} us ({len(durs[k])} dispatches) |")
+    if len(kernels) > 1 and call_us:
+        lines.append(f"| one call (sum of the above) | {call_us:.2f} us |")
+    if flops and call_us:
+        lines.append(f"| TFLOP/s = algorithmic flops / one call | {flops / (call_us * 1e-6) / 1e12:.1f} |")
+        lines.append(f"| fraction of the 2500 TFLOP/s bf16 dense peak | {flops / (call_us * 1e-6) / 1e12 / 2500:.4f} |")
+    for k in sorted(avg):
+        lines.append(f"| {k} | {avg[k]:.6g} |")
+    k0 = durs[kernels[0]]
+    us0 = sum(k0) / len(k0) if k0 else None
+    gui = avg.get("GRBM_GUI_ACTIVE")
+    if gui and us0:
+        cyc = gui / xcds
+        lines.append(f"| clock = GRBM_GUI_ACTIVE / {xcds} XCDs / duration | {cyc / us0 / 1e3:.3f} GHz |")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in avg:
+            lines.append(f"| MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / {xcds} x {cus} CUs x 4 SIMDs) | "
+                         f"{100 * avg['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * cus * 4):.1f} % |")
+        if "SQ_VALU_MFMA_COEXEC_CYCLES" in avg:
+            lines.append(f"| MFMA and VALU co-executing = SQ_VALU_MFMA_COEXEC_CYCLES / (same) | "
+                         f"{100 * avg['SQ_VALU_MFMA_COEXEC_CYCLES'] / (cyc * cus * 4):.1f} % |")
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in avg:
+            tf = avg["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512 / (us0 * 1e-6) / 1e12
+            peak = cus * 4 * 1024 * cyc / us0 * 1e-6  # 1024 bf16 flops per SIMD per clock
+            lines.append(f"| bf16 MFMA TFLOP/s executed (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 / duration) | {tf:.1f} |")
+            lines.append(f"| bf16 dense peak at the measured clock (1024 flops / SIMD / clock) | {peak:.1f} TFLOP/s |")
+    if "SQ_WAVE_CYCLES" in avg:
+        for k in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS"):
+            if k in avg:
+                lines.append(f"| {k} / SQ_WAVE_CYCLES | {100 * avg[k] / avg['SQ_WAVE_CYCLES']:.1f} % |")
+    if "SQ_INSTS_MFMA" in avg and "SQ_INSTS_VALU" in avg:
+        lines.append(f"| VALU instructions per MFMA (SQ_INSTS_VALU / SQ_INSTS_MFMA, MFMA included) | "
+                     f"{avg['SQ_INSTS_VALU'] / avg['SQ_INSTS_MFMA']:.2f} |")
+    print("\n".join(lines))
+
+
 def headline_bench(args, stream):
     """Config 3, the headline: one step = the 32 lm_attend calls of a tick."""
     import torch
@@ -514,7 +669,16 @@ def main():
     ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 CSV output directories (with --kernel, --last) and exit")
+    ap.add_argument("--kernel", nargs="+", default=["tiled_attn"],
+                    help="kernel name substrings of one call (--summarize); counters are read for the first")
+    ap.add_argument("--last", type=int, default=10)
+    ap.add_argument("--flops", type=float, default=None, help="algorithmic flops per dispatch (--summarize)")
     args = ap.parse_args()
+    if args.summarize:
+        summarize_profile(args.summarize, args.kernel, args.last, args.flops)
+        return
     if args.calib_copy_mib:
         copy_calibration(args.calib_copy_mib)
         return
@@ -549,10 +713,6 @@ def main():
             extra["config5_mha"] = dit_bench(stream, args.steps, args.warmup, hk=32)
             # the reference's signature (no workspace): the last round's tiles run as row halves
             extra["config5_no_workspace"] = dit_bench(stream, args.steps, args.warmup, split=False)
-        if args.only == 5:  # A/B of the tail split, alternating
-            for i in range(2):
-                extra[f"config5_unsplit_{i}"] = dit_bench(stream, args.steps, args.warmup, split=False)
-                extra[f"config5_split_{i}"] = dit_bench(stream, args.steps, args.warmup)
     if args.only in (0, 2):
         log("[bench] config 2 decode")
         b2 = DecodeBench(2, args.pools, chunk=args.chunk)
@@ -611,6 +771,8 @@ def main():
         log(f"[bench] cpu: {v:.2f} GB/s on {thr} threads")
         cpu = {"value": round(v, 3), "unit": "GB/s", "cores": thr, "kind": "port", "sample": sample,
                "seconds_per_sample": round(sec, 4)}
+        extra["cpu_baseline"] = cpu_baselines(cpu)
+        log(f"[bench] cpu, every config: {extra['cpu_baseline']}")
 
     out = {
         "metric": "decode attn HBM GB/s (% peak) @128 duplex sessions",

@@ -48,7 +48,8 @@ extern "C" {
  * of a captured graph of the same batch bucket. */
 typedef struct omni_attn_decode_plan {
   int32_t rows;     /* rows per launch (the batch bucket) */
-  int32_t hq, hk;   /* query heads, K/V heads (hq % hk == 0, hq / hk in {1,2,4,8}) */
+  int32_t hq, hk;   /* query heads, K/V heads (hq % hk == 0, hq / hk in {1,2,4}, as the
+                       reference's stack.rs:94-106 accepts) */
   int32_t page;     /* tokens per page, a power of two */
   int32_t max_len;  /* bound on keys any row sees; longer rows still run, slower */
   int32_t chunk;    /* keys per split (a multiple of 128) */

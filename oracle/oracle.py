@@ -44,9 +44,12 @@ def build() -> str:
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB):
+        # OMNI_ORACLE_LIB names another build of the same source (the
+        # sanitizer build of tests/c/Makefile).
+        path = os.environ.get("OMNI_ORACLE_LIB") or _LIB
+        if path == _LIB and not os.path.exists(_LIB):
             build()
-        L = ctypes.CDLL(_LIB)
+        L = ctypes.CDLL(path)
         P = ctypes.c_void_p
         i32, f32, i64, u64 = ctypes.c_int, ctypes.c_float, ctypes.c_int64, ctypes.c_uint64
         L.oracle_paged_attend.argtypes = [P, P, P, P, i32, P, P, i32, P, i32, i32, i32, f32, i32, i32]

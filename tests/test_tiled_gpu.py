@@ -54,6 +54,31 @@ def test_prefill_config4_subset(oracle):
     assert_close(run_prefill(c), oracle_paged(oracle, c), what="config4 subset")
 
 
+def test_prefill_config4_own_draw(oracle):
+    """Config 4's own seeded draw (B = 8, seed 4000: 25,499 rows, up to 4,563
+    keys), the workload bench.py times, so its work-list order (longest tiles
+    first, XCD ranges, the 8 sequences' items) is the one checked: the oracle
+    on the first and last 64 rows of every sequence plus 256 seeded random
+    rows, and the split-K decode kernel on every row."""
+    c = W.config_case(4)
+    assert c.rows == 25499 and len(c.extra["new"]) == 8
+    got = run_prefill(c)
+    starts = np.concatenate([[0], np.cumsum(c.extra["new"])])
+    idx = [np.arange(a, min(a + 64, b)) for a, b in zip(starts[:-1], starts[1:])]
+    idx += [np.arange(max(b - 64, a), b) for a, b in zip(starts[:-1], starts[1:])]
+    idx.append(np.random.default_rng(4001).choice(c.rows, 256, replace=False))
+    idx = np.unique(np.concatenate(idx))
+    want = oracle.paged_attend(np.ascontiguousarray(c.qkv[idx]), c.kv, c.pos[idx].copy(), c.seq[idx].copy(), 1,
+                               c.indptr, c.pages, c.page, c.hq, c.hk, c.scale, nthreads=16)
+    assert_close(got[idx], want, what=f"config4 {len(idx)} rows vs oracle")
+    plan = oa.decode_plan(c.rows, c.hq, c.hk, c.page, int(c.pos.max()) + 1)
+    out = torch.zeros(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    oa.qwen3_attend(dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), 1, dev_i32(c.indptr),
+                    dev_i32(c.pages), c.page, out, c.hq, c.hk, c.scale, plan, oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    assert_close(got, host_bits(out), what="config4 prefill vs decode, every row")
+
+
 def run_dense(c, b_all=True):
     q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
     out = torch.zeros(c.batch, c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda")
