@@ -71,6 +71,19 @@ int omni_qwen3_attend(const void* qkv, const void* kv, const int32_t* pos, const
                       const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
                       const omni_attn_decode_plan* plan, void* workspace, void* stream);
 
+/* omni_qwen3_attend without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc); it has no counterpart in the reference. The split partials go to
+ * a static 16 MiB device array the library holds on each GPU until the
+ * process ends (OMNI_ATTN_NOALLOC_SCRATCH_BYTES); a plan whose
+ * workspace_bytes exceeds it is rejected with OMNI_ATTN_EWORKSPACE. The call
+ * allocates nothing. All calls on one GPU share the array: calls that overlap
+ * on one GPU (concurrent streams) race. */
+#define OMNI_ATTN_NOALLOC_SCRATCH_BYTES (16LL << 20)
+int omni_qwen3_attend_noalloc(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                              const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk,
+                              float scale, const omni_attn_decode_plan* plan, void* stream);
+
 /* `lm_attend`'s semantics (crates/omni-personaplex/kernels/lm.cu:273-290) over
  * bf16 slots (the layout of attend.cuh's bf16 attend_row, attend.cuh:41-106):
  * MHA with `heads` query and K/V heads, qkv rows [3 heads][128], each row sees

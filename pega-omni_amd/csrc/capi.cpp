@@ -18,6 +18,8 @@
 
 #include "kernels.h"
 
+static_assert(OMNI_ATTN_NOALLOC_SCRATCH_BYTES == omni::kNoAllocScratchBytes, "static scratch size");
+
 namespace {
 
 thread_local char g_err[256] = "";
@@ -148,6 +150,22 @@ int omni_qwen3_attend(const void* qkv, const void* kv, const int32_t* pos, const
                       const omni_attn_decode_plan* plan, void* workspace, void* stream) {
   return decode_common(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, 0, 0, plan, workspace,
                        stream);
+}
+
+int omni_qwen3_attend_noalloc(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
+                              const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk,
+                              float scale, const omni_attn_decode_plan* plan, void* stream) {
+  if (!plan) return fail(OMNI_ATTN_EINVAL, "qwen3_attend_noalloc: null plan");
+  if (plan->workspace_bytes > omni::kNoAllocScratchBytes)
+    return fail(OMNI_ATTN_EWORKSPACE,
+                "qwen3_attend_noalloc: the plan needs %lld workspace bytes, above the %lld-byte static scratch "
+                "(fewer rows per call, or omni_qwen3_attend with a workspace)",
+                (long long)plan->workspace_bytes, (long long)omni::kNoAllocScratchBytes);
+  float* ws = nullptr;
+  if (plan->splits > 1 && plan->rows > 0 && omni::noalloc_scratch(&ws) != 0)
+    return fail(OMNI_ATTN_ELAUNCH, "qwen3_attend_noalloc: no device address for the static scratch: %s",
+                hipGetErrorString(omni::g_launch_status));
+  return decode_common(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, 0, 0, plan, ws, stream);
 }
 
 int omni_lm_attend(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,

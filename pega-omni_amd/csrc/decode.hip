@@ -21,6 +21,8 @@
 // (Merging in the last-arriving split workgroup needs a device-scope release
 // fence per workgroup, which writes back the L2 on gfx950 and costs far more
 // than the separate combine launch.)
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -557,6 +559,37 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
     decode_combine<<<dim3(a.hq, rows), kHead, 0, stream>>>(a);
     if (check_launch() != 0) return -3;
   }
+  return 0;
+}
+
+// ------------------------------------------------- allocation-free workspace
+//
+// Split partials for callers that cannot allocate (omni_qwen3_attend_noalloc):
+// a file-scope device array, one copy per GPU the library runs on, held until
+// the process ends. Host code never passes the array's name to a kernel (on
+// the host it only stands in for the symbol); it passes the device address
+// hipGetSymbolAddress returns, looked up once per device with that device
+// current. Every call on one GPU shares the array, so calls that overlap on
+// one GPU race. Nothing in it needs clearing: a split writes its partial
+// before decode_combine reads it, and combine reads only the splits a row has.
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+int noalloc_scratch(float** ptr) {
+  static std::mutex mu;
+  static float* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !p) {
+      g_launch_status = rc;
+      return -1;
+    }
+    addr[dev] = static_cast<float*>(p);
+  }
+  *ptr = addr[dev];
   return 0;
 }
 

@@ -41,6 +41,14 @@ struct DecodeArgs {
 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream);
 
+// The allocation-free decode entry point's split-partial workspace: a
+// file-scope device array of this many bytes per GPU.
+constexpr int64_t kNoAllocScratchBytes = 16LL << 20;
+constexpr int kMaxDevices = 64;
+// Device address of that array on the current device (looked up once per
+// device); 0 on success, -1 if the lookup fails.
+int noalloc_scratch(float** ptr);
+
 int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int shift,
                      const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
                      hipStream_t stream);

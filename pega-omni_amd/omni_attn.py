@@ -28,6 +28,7 @@ ETABLE = -5
 EXPORTS = (
     "omni_attn_decode_plan_init",
     "omni_qwen3_attend",
+    "omni_qwen3_attend_noalloc",
     "omni_lm_attend",
     "omni_lm_attend_fp8",
     "omni_attn_decode_run_lastlen",
@@ -116,6 +117,7 @@ def load(path: str | None = None):
     sig = {
         "omni_attn_decode_plan_init": [i32, i32, i32, i32, i32, i32, dplan],
         "omni_qwen3_attend": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
+        "omni_qwen3_attend_noalloc": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P],
         "omni_lm_attend": [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, dplan, P, P],
         "omni_lm_attend_fp8": [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, dplan, P, P],
         "omni_attn_decode_run_lastlen": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
@@ -234,6 +236,19 @@ def qwen3_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, sc
     _check(load().omni_qwen3_attend(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr),
                                     _ptr(pages), page, _ptr(out), hq, hk, float(scale), ctypes.byref(plan),
                                     _ptr(workspace), _stream(stream)))
+    return out
+
+
+def qwen3_attend_noalloc(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, scale, plan, stream=None):
+    """``qwen3_attend`` without a workspace argument: the split partials go to
+    the library's static per-GPU scratch (no allocation; calls that overlap on
+    one GPU race). No counterpart in the reference."""
+    _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
+    for t, n in ((pos, "pos"), (seq, "seq"), (indptr, "indptr"), (pages, "pages")):
+        _i32_dev(t, n)
+    _check(load().omni_qwen3_attend_noalloc(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr),
+                                            _ptr(pages), page, _ptr(out), hq, hk, float(scale), ctypes.byref(plan),
+                                            _stream(stream)))
     return out
 
 

@@ -96,6 +96,14 @@ static void check_decode_run_validation(void) {
   CHECK(omni_attn_decode_plan_init(4, 16, 8, 1, 16, 0, &d) == OMNI_ATTN_OK);
   CHECK(omni_qwen3_attend_dense(kFake, kFake, 1, 16, 16, kFake, 16, 8, 0.1f, &d, kFake, NULL) == OMNI_ATTN_EINVAL);
   CHECK(omni_qwen3_attend_dense(kFake, kFake, 4, 14, 32, kFake, 16, 8, 0.1f, &d, kFake, NULL) == OMNI_ATTN_EINVAL);
+  /* the allocation-free call: a plan above its static scratch is rejected */
+  omni_attn_decode_plan big;
+  CHECK(omni_attn_decode_plan_init(4096, 32, 32, 16, 65536, 128, &big) == OMNI_ATTN_OK);
+  CHECK(big.workspace_bytes > OMNI_ATTN_NOALLOC_SCRATCH_BYTES);
+  CHECK(omni_qwen3_attend_noalloc(kFake, kFake, kFake, NULL, 0, kFake, kFake, 16, kFake, 32, 32, 0.1f, &big, NULL) ==
+        OMNI_ATTN_EWORKSPACE);
+  CHECK(omni_qwen3_attend_noalloc(kFake, kFake, kFake, NULL, 0, kFake, kFake, 16, kFake, 32, 32, 0.1f, NULL, NULL) ==
+        OMNI_ATTN_EINVAL);
   /* a zero-row plan is a no-op */
   omni_attn_decode_plan z;
   CHECK(omni_attn_decode_plan_init(0, 16, 8, 16, 100, 0, &z) == OMNI_ATTN_OK);
