@@ -69,19 +69,23 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, int bytes = -1) {
 // against LDS reads and falls back to lgkmcnt(0) before every LDS operand read
 // while one is in flight. Out of its sight, the reads keep their partial waits;
 // the kernel waits for these loads itself (vmcnt(0) before each tile barrier).
-// M0 (the LDS base of a DMA) is an input operand, so the compiler sets it; the
-// s_nop covers the M0-write-to-DMA hazard.
+// M0 (the LDS base of a DMA) is an input operand, so the compiler sets it.
+// The compiler's hazard recognizer does not see inside the asm, so the asm
+// carries its own wait states: s_nop 4 (five) covers both the M0 write and a
+// VALU write (v_readfirstlane) of the resource SGPRs right before the load,
+// which a VMEM read of an SGPR needs five wait states after; with fewer the
+// load can use a stale base address.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_void*)p;
 }
 __device__ __forceinline__ void dma_buffer16(i32x4 rsrc, uint32_t voff, const void* lds) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(rsrc), "{m0}"(lds_addr(lds))
                : "memory");
 }
 __device__ __forceinline__ void dma_global16(const void* src, const void* lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(src), "{m0}"(lds_addr(lds))
                : "memory");
