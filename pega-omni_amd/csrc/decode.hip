@@ -483,7 +483,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
 }
 
 // Merge the splits of every (row, q head) that used more than one: a
-// workgroup of 128 threads per (q head, row), one thread per dim.
+// workgroup of 128 threads per (q head, row), one thread per dim. A thread's
+// loads (the row's split lse values and its dim of every split's partial) are
+// all issued before any is used, so the merge costs one memory round trip
+// rather than one per split (up to kCombineBatch splits per round trip).
+constexpr int kCombineBatch = 8;
+
 __global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
   const int h = blockIdx.x, n = blockIdx.y, d = threadIdx.x;
   const int s = a.ragged ? a.seq[n] : n;
@@ -492,13 +497,30 @@ __global__ __launch_bounds__(kHead) void decode_combine(DecodeArgs a) {
   if (nsplit <= 1) return;
   const int64_t hh = (int64_t)n * a.hq + h;
   const float* lse = a.ws_lse + hh * a.splits;
-  float top = -INFINITY;
-  for (int i = 0; i < nsplit; ++i) top = fmaxf(top, lse[i]);
-  float num = 0.f, den = 0.f;
-  for (int i = 0; i < nsplit; ++i) {
-    const float w = fast_exp2(lse[i] - top);
-    den += w;
-    num = fmaf(w, a.ws_o[(hh * a.splits + i) * kHead + d], num);
+  const float* po = a.ws_o + hh * a.splits * kHead + d;
+  float top = -INFINITY, num = 0.f, den = 0.f;
+  for (int i0 = 0; i0 < nsplit; i0 += kCombineBatch) {
+    float lv[kCombineBatch], ov[kCombineBatch];
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const bool in = i0 + k < nsplit;
+      lv[k] = in ? lse[i0 + k] : -INFINITY;
+      ov[k] = in ? po[(int64_t)(i0 + k) * kHead] : 0.f;
+    }
+    float bt = top;
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) bt = fmaxf(bt, lv[k]);
+    // Rescale what earlier batches summed to this batch's running max.
+    const float c = top == -INFINITY ? 0.f : fast_exp2(top - bt);
+    num *= c;
+    den *= c;
+#pragma unroll
+    for (int k = 0; k < kCombineBatch; ++k) {
+      const float w = lv[k] == -INFINITY ? 0.f : fast_exp2(lv[k] - bt);
+      den += w;
+      num = fmaf(w, ov[k], num);
+    }
+    top = bt;
   }
   a.out[hh * kHead + d] = (bf16_t)f2bf(num / den);
 }
