@@ -566,7 +566,7 @@ def copy_calibration(mb):
     print(json.dumps({"copy_calibration_mib": mb, "bytes_read": mb << 20, "bytes_written": mb << 20}))
 
 
-def summarize_profile(dirs, kernels, last, flops=None, cus=256, xcds=8):
+def summarize_profile(dirs, kernels, last, flops=None, cus=256, xcds=8, nbytes=None):
     """Summarise rocprofv3 CSV output (one directory per pass) for the last
     `last` dispatches of each kernel whose name contains one of `kernels`
     (the timed calls of a bench.py run: its warmup calls come first). Prints a
@@ -604,6 +604,9 @@ def summarize_profile(dirs, kernels, last, flops=None, cus=256, xcds=8):
             lines.append(f"| kernel-trace duration of `{k}` | {us:.2f} us ({len(durs[k])} dispatches) |")
     if len(kernels) > 1 and call_us:
         lines.append(f"| one call (sum of the above) | {call_us:.2f} us |")
+    if nbytes and call_us:
+        lines.append(f"| GB/s = algorithmic bytes / one call | {nbytes / (call_us * 1e-6) / 1e9:.1f} |")
+        lines.append(f"| fraction of the 8000 GB/s HBM peak | {nbytes / (call_us * 1e-6) / 1e9 / 8000:.4f} |")
     if flops and call_us:
         lines.append(f"| TFLOP/s = algorithmic flops / one call | {flops / (call_us * 1e-6) / 1e12:.1f} |")
         lines.append(f"| fraction of the 2500 TFLOP/s bf16 dense peak | {flops / (call_us * 1e-6) / 1e12 / 2500:.4f} |")
@@ -648,8 +651,9 @@ def headline_bench(args, stream):
     total_bytes = sum(b.bytes_per_layer)
     log(f"[bench] config {cfg}: {ms:.3f} ms/step, {total_bytes / (ms * 1e-3) / 1e9:.0f} GB/s, "
         f"launch {launch_ms*1e3:.1f} us")
-    g = graph_step_ms(lambda s, e: b.step(s, e), args.steps, args.warmup, stream)
-    log(f"[bench] config {cfg} as a replayed HIP graph: {g:.3f} ms/step")
+    g = None if args.no_graph else graph_step_ms(lambda s, e: b.step(s, e), args.steps, args.warmup, stream)
+    if g is not None:
+        log(f"[bench] config {cfg} as a replayed HIP graph: {g:.3f} ms/step")
     c = b.cases[0]
     head = dict(ms=ms, launch_ms=launch_ms, total_bytes=total_bytes, layers=b.layers, sessions=c.rows,
                 heads=f"{c.hq}q/{c.hk}kv", kv_pools=len(b.pools), chunk=b.plan.chunk, graph_ms=g)
@@ -666,6 +670,8 @@ def main():
     ap.add_argument("--pools", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the HIP-graph replays (profiling runs: the trace then ends on the timed calls)")
     ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
@@ -674,10 +680,11 @@ def main():
     ap.add_argument("--kernel", nargs="+", default=["tiled_attn"],
                     help="kernel name substrings of one call (--summarize); counters are read for the first")
     ap.add_argument("--last", type=int, default=10)
-    ap.add_argument("--flops", type=float, default=None, help="algorithmic flops per dispatch (--summarize)")
+    ap.add_argument("--flops", type=float, default=None, help="algorithmic flops per call (--summarize)")
+    ap.add_argument("--bytes", type=float, default=None, help="algorithmic bytes per call (--summarize)")
     args = ap.parse_args()
     if args.summarize:
-        summarize_profile(args.summarize, args.kernel, args.last, args.flops)
+        summarize_profile(args.summarize, args.kernel, args.last, args.flops, nbytes=args.bytes)
         return
     if args.calib_copy_mib:
         copy_calibration(args.calib_copy_mib)
@@ -717,7 +724,8 @@ def main():
         log("[bench] config 2 decode")
         b2 = DecodeBench(2, args.pools, chunk=args.chunk)
         ms2, l2 = time_steps(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream, per_launch=b2.layers)
-        g2 = graph_step_ms(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream)
+        g2 = float("nan") if args.no_graph else graph_step_ms(lambda s, e: b2.step(s, e), args.steps, args.warmup,
+                                                               stream)
         tb = sum(b2.bytes_per_layer)
         extra["config2"] = dict(workload="config2: " + __import__("workloads").CONFIGS[2]["desc"],
                                 ms_per_step=round(ms2, 4), gbs=round(tb / (ms2 * 1e-3) / 1e9, 1),
@@ -732,7 +740,8 @@ def main():
         log("[bench] config 3 decode over FP8 E4M3 slots")
         b8 = DecodeBench(3, args.pools, chunk=args.chunk, fp8=True)
         ms8, l8 = time_steps(lambda s, e: b8.step(s, e), args.steps, args.warmup, stream, per_launch=b8.layers)
-        g8 = graph_step_ms(lambda s, e: b8.step(s, e), args.steps, args.warmup, stream)
+        g8 = float("nan") if args.no_graph else graph_step_ms(lambda s, e: b8.step(s, e), args.steps, args.warmup,
+                                                               stream)
         tb = sum(b8.bytes_per_layer)
         extra["config3_fp8"] = dict(workload="config3 over PersonaPlex FP8 E4M3 slots (8448 B per slot)",
                                     ms_per_step=round(ms8, 4), gbs=round(tb / (ms8 * 1e-3) / 1e9, 1),
@@ -808,7 +817,7 @@ def main():
             "launch_us": round(launch_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
-        "extra": dict(extra, config3_graph=dict(
+        "extra": dict(extra, config3_graph=None if head["graph_ms"] is None else dict(
             ms_per_step=round(head["graph_ms"], 4), gbs=round(total_bytes / (head["graph_ms"] * 1e-3) / 1e9, 1),
             note="the same step captured once as a HIP graph and replayed (the engines' per-bucket graphs)")),
     }
