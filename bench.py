@@ -175,11 +175,12 @@ def graph_step_ms(run_step, steps, warmup, stream):
     return start.elapsed_time(end) / steps
 
 
-def cpu_decode_baseline(cfg=3, rows=32, min_seconds=10.0, threads=None):
+def cpu_decode_baseline(cfg=3, rows=None, min_seconds=10.0, threads=None):
     """The oracle (a C port of the reference math) timed on this host's cores on
-    a bounded sample of the decode workload: the first `rows` sessions of one
-    layer (their pages compacted into a pool of exactly that size), repeated
-    for at least `min_seconds`. Returns (GB/s, seconds per rep, threads, text)."""
+    one layer of the decode workload: the first `rows` sessions (all of them
+    by default), their pages compacted into a pool of exactly that size,
+    repeated for at least `min_seconds`. Returns (GB/s, seconds per rep,
+    threads, text)."""
     import numpy as np
 
     import oracle
@@ -187,6 +188,7 @@ def cpu_decode_baseline(cfg=3, rows=32, min_seconds=10.0, threads=None):
 
     threads = threads or min(16, os.cpu_count() or 1)
     c = W.config_case(cfg, values=None)
+    rows = rows or c.rows
     c.pos, c.seq = c.pos[:rows].copy(), c.seq[:rows].copy()
     used = int(c.indptr[rows])
     c.indptr = c.indptr[: rows + 1].copy()
@@ -207,10 +209,12 @@ def cpu_decode_baseline(cfg=3, rows=32, min_seconds=10.0, threads=None):
 
 def _timing_values(rng, n):
     """Normal bf16 bit patterns in +-[1/8, 2) with random sign and mantissa:
-    inputs for CPU timing only (their outputs are not checked)."""
+    inputs for CPU timing only (their outputs are not checked). Up to 2^25
+    values are drawn and repeated to length n."""
     import numpy as np
 
-    return (rng.integers(0, 1 << 16, n, dtype=np.uint16) & np.uint16(0x81FF)) | np.uint16(0x3E00)
+    block = (rng.integers(0, 1 << 16, min(n, 1 << 25), dtype=np.uint16) & np.uint16(0x81FF)) | np.uint16(0x3E00)
+    return block if block.size == n else np.resize(block, n)
 
 
 def _repeat(fn, min_seconds):
@@ -286,8 +290,9 @@ def cpu_model():
 
 def cpu_baselines(head_cpu):
     """The CPU path (the oracle, a C port of the reference math) on every
-    BASELINE config: config 1 in full, one config 2 layer, config 3's sample
-    (the headline's cpu_baseline), and bounded samples of configs 4 and 5."""
+    BASELINE config: one full layer of configs 1 and 2, config 3's (the
+    headline's cpu_baseline, also a full layer), and bounded samples of
+    configs 4 and 5."""
     out = {"cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
     for cfg, rows, secs in ((1, 4, 3.0), (2, 64, 3.0)):
         v, sec, thr, text = cpu_decode_baseline(cfg, rows=rows, min_seconds=secs)
