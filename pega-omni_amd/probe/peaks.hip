@@ -8,19 +8,43 @@
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Four independent 32x32x16 bf16 MFMA chains per wave, `iters` rounds.
+__device__ inline uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  return x ^ (x >> 16);
+}
+
+// Four independent 32x32x16 bf16 MFMA chains per wave, `iters` rounds of four
+// steps. RANDOM = false: one smooth operand pair (few bits change between
+// lanes). RANDOM = true: four operand pairs of hashed values uniform in
+// [-2, 2), rotated between the steps, as attention tiles feed the MFMAs. The
+// card lowers its clock under MFMA load by how many operand bits toggle, so
+// the random form is the ceiling real data reaches.
+template <bool RANDOM>
 __global__ __launch_bounds__(256) void mfma_loop(float* sink, int iters) {
-  bf16x8 a, b;
-  for (int i = 0; i < 8; ++i) {
-    a[i] = (__bf16)(0.001f * (threadIdx.x + i));
-    b[i] = (__bf16)(0.002f * (threadIdx.x - i));
-  }
+  bf16x8 a[4], b[4];
+  for (int s = 0; s < 4; ++s)
+    for (int i = 0; i < 8; ++i) {
+      float x = 0.001f * (threadIdx.x + i), y = 0.002f * (threadIdx.x - i);
+      if (RANDOM) {
+        const uint32_t h = mix32(threadIdx.x * 977u + blockIdx.x * 131071u + s * 8u + i), g = mix32(h);
+        x = ((int)(h & 0xffff) - 32768) / 16384.f;
+        y = ((int)(g & 0xffff) - 32768) / 16384.f;
+      }
+      a[s][i] = (__bf16)x;
+      b[s][i] = (__bf16)y;
+    }
   f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
   for (int it = 0; it < iters; ++it) {
-    c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c0, 0, 0, 0);
-    c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c1, 0, 0, 0);
-    c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c2, 0, 0, 0);
-    c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c3, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s], b[s], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(s + 1) & 3], b[s], c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(s + 2) & 3], b[(s + 1) & 3], c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(s + 3) & 3], b[(s + 2) & 3], c3, 0, 0, 0);
+    }
   }
   float s = 0.f;
   for (int i = 0; i < 16; ++i) s += c0[i] + c1[i] + c2[i] + c3[i];
@@ -76,8 +100,12 @@ int omni_peaks_lds(void* sink, int blocks, int iters, void* stream) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 // Each returns 0 or -1; the caller times the launch on `stream`.
-int omni_peaks_mfma(void* sink, int blocks, int iters, void* stream) {
-  mfma_loop<<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
+// 16 MFMAs per wave per iteration; random != 0 selects the random operands.
+int omni_peaks_mfma(void* sink, int blocks, int iters, int random, void* stream) {
+  if (random)
+    mfma_loop<true><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
+  else
+    mfma_loop<false><<<blocks, 256, 0, (hipStream_t)stream>>>((float*)sink, iters);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 int omni_peaks_valu(void* sink, int blocks, int iters, int exp, void* stream) {
