@@ -201,7 +201,8 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
 /* Replaces `hidream_attend` (crates/omni-hidream-o1/kernels/hidream.cu:209-347).
  * q rows at q + n * q_stride + h * 128 (h < hq = G * hk), k and v [slots][hk][128],
  * out [q_len][hq][128]; row n sees the first *kv_len_at keys, with causal
- * only keys 0..n. The reference fixes G = 4 and hk = gridDim.y; here hq and hk
+ * only keys 0..n. A row that sees no key (*kv_len_at = 0) stores NaN, as the
+ * reference's 1 / l does. The reference fixes G = 4 and hk = gridDim.y; here hq and hk
  * are arguments (G in {1,2,4,8}). When the last round of tiles would fill at
  * most half the GPU, its tiles run as two workgroups of half the rows each
  * (no workspace; each row is computed the same way). */

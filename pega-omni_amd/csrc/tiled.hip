@@ -510,9 +510,10 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     if (h == 0) *reinterpret_cast<float2*>(seg + kBM * kHead + 2 * r) = make_float2(m, l);
     return;
   }
-  // Normalise and store.
+  // Normalise and store. A row that sees no key (*kv_len_at = 0) has l = 0 and
+  // O = 0, and stores 0 * (1 / 0) = NaN, as hidream.cu:333-346 does.
   if (!row_ok) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = 1.f / l;
   bf16_t* dst = t.out + ((int64_t)p * a.hq + head) * kHead;
 #pragma unroll
   for (int md = 0; md < 4; ++md)
@@ -561,7 +562,8 @@ __global__ __launch_bounds__(256) void dit_combine(TiledArgs a, int ntiles) {
     num[6] = fmaf(v1.z, w, num[6]);
     num[7] = fmaf(v1.w, w, num[7]);
   }
-  const float inv = den > 0.f ? 1.f / den : 0.f;
+  // den = 0 only when no chunk saw a key: NaN, as the unsplit kernel stores.
+  const float inv = 1.f / den;
   uint4 o;
   o.x = pack_bf16x2(num[0] * inv, num[1] * inv);
   o.y = pack_bf16x2(num[2] * inv, num[3] * inv);

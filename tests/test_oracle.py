@@ -193,6 +193,15 @@ def test_dense_kv_len_masks_tail(oracle):
     assert np.array_equal(a, b)
 
 
+
+def test_dense_no_key_gives_nan(oracle):
+    """*kv_len_at = 0: no row sees a key, so l stays 0 and the reference's
+    normalisation 1 / l (hidream.cu:337-346) turns O = 0 into NaN everywhere."""
+    case = W.dense_case(8, 2, 5, 40, 1, seed=23)
+    for causal in (0, 1):
+        got = oracle.dense_attend(case.q[0], case.k[0], case.v[0], 5, 0, case.q_stride, 8, 2, causal, case.scale_log2)
+        assert np.isnan(bits_to_f64(got)).all()
+
 # ------------------------------------------------------- FP8 (E4M3) ring attention
 def test_e4m3_decode_matches_torch(oracle):
     codes = np.arange(256, dtype=np.uint8)

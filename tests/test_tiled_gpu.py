@@ -7,6 +7,7 @@ import torch
 import omni_attn as oa
 import workloads as W
 from gpu_util import assert_close, dev_bits, dev_i32, host_bits
+from refs import bits_to_f64
 
 pytestmark = pytest.mark.gpu
 
@@ -194,6 +195,49 @@ def test_dit_row_halves_match_split(oracle, causal):
                                np.ascontiguousarray(c.v[0]), 128, 1024, c.q_stride, 32, 8, 0, c.scale_log2,
                                nthreads=16)
     assert_close(got[-128:], want, what=f"halves tail vs oracle c{causal}")
+
+
+@pytest.mark.parametrize("causal", [0, 1])
+def test_dit_no_key_gives_nan(oracle, causal):
+    """*kv_len_at = 0 (hidream.cu:337-346: l = 0, so O * (1 / l) = NaN): every
+    output element is NaN through the plain call, the batched call (row halves
+    for the last round) and the workspace call (key chunks, all empty), as the
+    oracle gives; a second call with keys overwrites them with finite values."""
+    c = W.dense_case(32, 8, 300, 300, causal, batch=2, seed=41 + causal)
+    want = oracle.dense_attend(np.ascontiguousarray(c.q[0]), np.ascontiguousarray(c.k[0]), np.ascontiguousarray(c.v[0]),
+                               c.q_len, 0, c.q_stride, c.hq, c.hk, causal, c.scale_log2, nthreads=16)
+    assert np.isnan(bits_to_f64(want)).all()
+    q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
+    zero = dev_i32(np.array([0], np.int32))
+    bs = (c.q_len * c.q_stride, c.kv_len * c.hk * 128, c.q_len * c.hq * 128)
+    outs = [torch.zeros(c.batch, c.q_len, c.hq * 128, dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    oa.hidream_attend(q, k, v, outs[0], c.q_len, zero, c.q_stride, causal, c.scale_log2, c.hq, c.hk)
+    oa.hidream_attend_batched(q, k, v, outs[1], c.q_len, zero, c.q_stride, causal, c.scale_log2, c.hq, c.hk, 2, *bs)
+    oa.hidream_attend_ws(q, k, v, outs[2], c.q_len, zero, c.q_stride, causal, c.scale_log2, c.hq, c.hk, 2, *bs,
+                         oa.hidream_workspace())
+    torch.cuda.synchronize()
+    assert np.isnan(bits_to_f64(host_bits(outs[0][0]))).all(), "plain call"
+    assert np.isnan(bits_to_f64(host_bits(outs[1]))).all(), "batched call"
+    assert np.isnan(bits_to_f64(host_bits(outs[2]))).all(), "workspace call"
+    # The same buffers with keys again: finite and equal to the oracle.
+    oa.hidream_attend_ws(q, k, v, outs[2], c.q_len, dev_i32(np.array([c.kv_len], np.int32)), c.q_stride, causal,
+                         c.scale_log2, c.hq, c.hk, 2, *bs, oa.hidream_workspace())
+    torch.cuda.synchronize()
+    assert_close(host_bits(outs[2])[1], oracle_dense(oracle, c, 1), what="keys again")
+
+
+def test_dit_empty_query_launch_is_a_no_op():
+    """q_len = 0 (and batch = 0) returns OK and writes nothing."""
+    c = W.dense_case(32, 8, 4, 4, 0, seed=43)
+    q, k, v = dev_bits(c.q), dev_bits(c.k), dev_bits(c.v)
+    out = torch.full((4, c.hq * 128), 3.0, dtype=torch.bfloat16, device="cuda")
+    kvl = dev_i32(np.array([4], np.int32))
+    oa.hidream_attend(q, k, v, out, 0, kvl, c.q_stride, 0, c.scale_log2, c.hq, c.hk)
+    oa.hidream_attend_ws(q, k, v, out, 0, kvl, c.q_stride, 0, c.scale_log2, c.hq, c.hk, 1, 0, 0, 0,
+                         oa.hidream_workspace())
+    oa.hidream_attend_batched(q, k, v, out, 4, kvl, c.q_stride, 0, c.scale_log2, c.hq, c.hk, 0, 0, 0, 0)
+    torch.cuda.synchronize()
+    assert bool((out == 3.0).all())
 
 
 @pytest.mark.parametrize("page", [1, 2, 4, 8, 64])
