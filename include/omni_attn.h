@@ -14,7 +14,11 @@
  *     allocate, never synchronise the host, and are safe to capture in a HIP
  *     graph: lengths are read from device arrays at run time;
  *   - `*_plan` calls are pure host code: they validate shapes and size the
- *     workspace; the caller owns and allocates the workspace.
+ *     workspace; the caller owns and allocates the workspace. A run takes the
+ *     plan its `*_plan_init` filled; a plan whose fields disagree with each
+ *     other is refused (OMNI_ATTN_EINVAL) before anything is launched;
+ *   - bf16 row buffers (qkv, q, k, v, kv, out) are 16-byte aligned (FP8 K/V
+ *     slots 8-byte), and batch strides are multiples of 8 elements.
  *
  * Layouts are the reference's (paths in the pega-omni tree):
  *   qkv row n: [(hq + 2 hk)][128] bf16, q heads first (qwen3.cu:5-7, lm.cu:285);

@@ -6,14 +6,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <new>
 #include <array>
 #include <climits>
-#include <vector>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <vector>
 
 #include "kernels.h"
@@ -54,7 +53,7 @@ hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 int pick_chunk(int rows, int hk, int max_len) {
   int chunk = 1024;
   while (chunk > 128) {
-    const long long units = (long long)rows * hk * ((max_len + chunk - 1) / chunk);
+    const long long units = (long long)rows * hk * (((long long)max_len + chunk - 1) / chunk);
     if (units >= 2048) break;
     chunk /= 2;
   }
@@ -69,10 +68,22 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   if (plan->hq != hq || plan->hk != hk || plan->page != page)
     return fail(OMNI_ATTN_EINVAL, "decode: plan was made for hq=%d hk=%d page=%d, called with hq=%d hk=%d page=%d",
                 plan->hq, plan->hk, plan->page, hq, hk, page);
+  // The kernels size their grid and the split partials from the plan, so a
+  // plan edited or built by hand must still be the one decode_plan_init
+  // would have made for its (rows, max_len, chunk).
+  if (plan->rows < 0 || plan->rows > 65535 || plan->max_len <= 0 || plan->chunk <= 0 || plan->chunk % 128 != 0 ||
+      plan->splits != ((int64_t)plan->max_len + plan->chunk - 1) / plan->chunk ||
+      (plan->splits > 1 &&
+       plan->workspace_bytes < (int64_t)plan->rows * hq * plan->splits * (OMNI_ATTN_HEAD_DIM + 1) * (int64_t)sizeof(float)))
+    return fail(OMNI_ATTN_EINVAL, "decode: plan is not self-consistent (rows=%d max_len=%d chunk=%d splits=%d workspace=%lld)",
+                plan->rows, plan->max_len, plan->chunk, plan->splits, (long long)plan->workspace_bytes);
   if (plan->rows == 0) return ok();
   const bool dense = len_mode == 2;
   if (!qkv || !kv || !out || (!dense && (!pos || !indptr || !pages || (ragged && !seq))))
     return fail(OMNI_ATTN_EINVAL, "decode: null device pointer");
+  if (((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(out)) & 15) != 0 ||
+      (reinterpret_cast<uintptr_t>(kv) & (fp8 ? 7 : 15)) != 0)
+    return fail(OMNI_ATTN_EINVAL, "decode: qkv and out must be 16-byte aligned, kv %d-byte aligned", fp8 ? 8 : 16);
   if (plan->splits > 1 && (!workspace || plan->workspace_bytes <= 0))
     return fail(OMNI_ATTN_EWORKSPACE, "decode: plan needs %lld workspace bytes", (long long)plan->workspace_bytes);
   if (!std::isfinite(scale)) return fail(OMNI_ATTN_EINVAL, "decode: non-finite scale");
@@ -139,7 +150,7 @@ int omni_attn_decode_plan_init(int rows, int hq, int hk, int page, int max_len, 
   plan->page = page;
   plan->max_len = max_len;
   plan->chunk = chunk;
-  plan->splits = (max_len + chunk - 1) / chunk;
+  plan->splits = (int32_t)(((int64_t)max_len + chunk - 1) / chunk);
   plan->workspace_bytes =
       plan->splits > 1 ? (int64_t)rows * hq * plan->splits * (OMNI_ATTN_HEAD_DIM + 1) * (int64_t)sizeof(float) : 0;
   return ok();
@@ -260,8 +271,11 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   std::vector<std::array<int32_t, 4>> tl;
   for (int n = 0; n < rows;) {
     int e = n + 1;
-    if (pos_h[n] < 0) return fail(OMNI_ATTN_ETABLE, "prefill_plan: row %d at negative position %d", n, pos_h[n]);
-    while (e < rows && seq_h[e] == seq_h[n] && pos_h[e] == pos_h[e - 1] + 1) ++e;
+    if (pos_h[n] < 0 || pos_h[n] == INT_MAX)
+      return fail(OMNI_ATTN_ETABLE, "prefill_plan: row %d at position %d outside [0, INT_MAX)", n, pos_h[n]);
+    if (seq_h[n] < 0) return fail(OMNI_ATTN_ETABLE, "prefill_plan: row %d names sequence %d", n, seq_h[n]);
+    while (e < rows && seq_h[e] == seq_h[n] && (int64_t)pos_h[e] == (int64_t)pos_h[e - 1] + 1 && pos_h[e] != INT_MAX)
+      ++e;
     for (int f = n; f < e; f += per_tile) {
       const int nq = (e - f) < per_tile ? (e - f) : per_tile;
       tl.push_back({seq_h[n], f, nq, pos_h[f + nq - 1] + 1});
@@ -315,9 +329,15 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
                           const int32_t* seq, const int32_t* indptr, const int32_t* pages, void* out, float scale,
                           const int32_t* work, void* stream) {
   if (!plan) return fail(OMNI_ATTN_EINVAL, "prefill_run: null plan");
+  if (plan->tiles < 0 || plan->workgroups < 0 || plan->hk <= 0 || plan->hq <= 0 || plan->hq % plan->hk != 0 ||
+      !pow2(plan->page))
+    return fail(OMNI_ATTN_EINVAL, "prefill_run: plan is not one prefill_plan_init made (tiles=%d hq=%d hk=%d page=%d)",
+                plan->tiles, plan->hq, plan->hk, plan->page);
   if (plan->tiles == 0) return ok();
   if (!qkv || !kv || !pos || !seq || !indptr || !pages || !out || !work)
     return fail(OMNI_ATTN_EINVAL, "prefill_run: null device pointer");
+  if (((reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(kv) | reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+    return fail(OMNI_ATTN_EINVAL, "prefill_run: qkv, kv and out must be 16-byte aligned");
   omni::TiledArgs a{};
   a.q = static_cast<const omni::bf16_t*>(qkv);
   a.q_stride = (int64_t)(plan->hq + 2 * plan->hk) * OMNI_ATTN_HEAD_DIM;
@@ -340,6 +360,20 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
 }
 
 namespace {
+
+// The DiT kernels move q, K, V and out rows in 16-byte pieces: every base and
+// every batch stride (elements) must keep 16-byte alignment.
+int dit_alignment(const void* q, const void* k, const void* v, const void* out, int batch, int64_t q_bstride,
+                  int64_t kv_bstride, int64_t out_bstride) {
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(out);
+  if ((bits & 15) != 0) return fail(OMNI_ATTN_EINVAL, "hidream_attend: q, k, v and out must be 16-byte aligned");
+  if (batch > 1 && (q_bstride < 0 || kv_bstride < 0 || out_bstride < 0 || q_bstride % 8 != 0 ||
+                    kv_bstride % 8 != 0 || out_bstride % 8 != 0))
+    return fail(OMNI_ATTN_EINVAL, "hidream_attend: batch strides %lld / %lld / %lld are not multiples of 8 elements",
+                (long long)q_bstride, (long long)kv_bstride, (long long)out_bstride);
+  return 0;
+}
 
 // Workgroups of the tiled kernel resident at once on the current device (one per CU).
 int resident_tiled_groups() {
@@ -365,6 +399,7 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
   if (q_stride < hq * OMNI_ATTN_HEAD_DIM || q_stride % 8 != 0)
     return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_stride=%d", q_stride);
   if (batch > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: batch=%d", batch);
+  if (int rc = dit_alignment(q, k, v, out, batch, q_bstride, kv_bstride, out_bstride)) return rc;
   omni::TiledArgs a{};
   a.q = static_cast<const omni::bf16_t*>(q);
   a.q_stride = q_stride;
@@ -408,6 +443,7 @@ int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* ou
   if (q_stride < hq * OMNI_ATTN_HEAD_DIM || q_stride % 8 != 0)
     return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_stride=%d", q_stride);
   if (batch > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: batch=%d", batch);
+  if (int rc = dit_alignment(q, k, v, out, batch, q_bstride, kv_bstride, out_bstride)) return rc;
   if ((reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
     return fail(OMNI_ATTN_EINVAL, "hidream_attend: workspace must be 16-byte aligned");
   omni::TiledArgs a{};
@@ -706,11 +742,15 @@ int omni_attn_rows_push(omni_attn_rows* r, const int32_t* page_ids, int npages, 
   // Every row's slot must lie in the lease.
   const int64_t last = count > 0 ? (int64_t)first + count - 1 : -1;
   const int64_t reach = r->ring > 0 ? std::min<int64_t>(last, r->ring - 1) : last;
+  if (last > INT32_MAX) return fail(OMNI_ATTN_EINVAL, "rows_push: position %lld past int32", (long long)last);
   if (count > 0 && reach / r->page >= npages)
     return fail(OMNI_ATTN_ETABLE, "rows_push: position %lld needs page %lld of a %d-page lease", (long long)last,
                 (long long)(reach / r->page), npages);
   if (r->pos.size() + (size_t)count > (size_t)INT32_MAX || r->pages.size() + (size_t)npages > (size_t)INT32_MAX)
     return fail(OMNI_ATTN_EINVAL, "rows_push: too many rows or pages");
+  for (int i = 0; i < npages; ++i)
+    if ((int64_t)page_ids[i] * r->page + r->page - 1 > INT32_MAX)
+      return fail(OMNI_ATTN_ETABLE, "rows_push: page id %d puts slots past int32", page_ids[i]);
   if (r->indptr.empty()) r->indptr.push_back(0);
   for (int i = 0; i < count; ++i) {
     const int64_t p = (int64_t)first + i;

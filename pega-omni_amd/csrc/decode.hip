@@ -600,7 +600,11 @@ int noalloc_scratch(float** ptr) {
   static std::mutex mu;
   static float* addr[kMaxDevices] = {};
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+  const hipError_t drc = hipGetDevice(&dev);
+  if (drc != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    g_launch_status = drc != hipSuccess ? drc : hipErrorInvalidDevice;
+    return -1;
+  }
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[dev]) {
     void* p = nullptr;

@@ -227,3 +227,75 @@ def test_short_entry_points_validate_before_launch():
     assert L.omni_codec_attention(f, f, f, f, f, 4, 1024, 8, -1.0, None) == oa.EINVAL
     assert L.omni_lm_dep_kv_attend(f, f, 8, f, 4, 16, 0.125, None) == oa.EINVAL
     assert L.omni_lm_dep_kv_attend(f, f, 0, f, 0, 16, 0.125, None) == oa.OK
+
+
+def test_decode_rejects_a_plan_edited_after_init():
+    """The kernels size their grid and split partials from the plan: a plan
+    whose fields no longer agree (more splits than its chunk gives, a chunk
+    off the 128-key grid, a workspace smaller than its splits need, rows past
+    the grid limit) is refused before any launch."""
+    L = oa.load()
+    fake = ctypes.c_void_p(4096)
+
+    def run(p):
+        return L.omni_qwen3_attend(fake, fake, fake, None, 0, fake, fake, 16, fake, 16, 8, 0.1, ctypes.byref(p), fake,
+                                   None)
+
+    for field, value in [("splits", 9), ("chunk", 100), ("chunk", 0), ("workspace_bytes", 1024), ("rows", 70000),
+                         ("max_len", 0)]:
+        p = oa.decode_plan(4, 16, 8, 16, 1000, chunk=128)
+        setattr(p, field, value)
+        assert run(p) == oa.EINVAL, field
+        assert "self-consistent" in L.omni_attn_last_error().decode()
+
+
+def test_entry_points_reject_misaligned_rows():
+    """Rows move in 16-byte pieces: q / qkv, k, v, kv, out at 16-byte
+    alignment (FP8 slots at 8), and DiT batch strides in multiples of 8
+    elements. All refused before any launch."""
+    L = oa.load()
+    f, odd, eight = ctypes.c_void_p(4096), ctypes.c_void_p(4098), ctypes.c_void_p(4104)
+    p = oa.decode_plan(4, 16, 8, 16, 1000, chunk=128)
+    assert L.omni_qwen3_attend(odd, f, f, None, 0, f, f, 16, f, 16, 8, 0.1, ctypes.byref(p), f, None) == oa.EINVAL
+    assert L.omni_qwen3_attend(f, eight, f, None, 0, f, f, 16, f, 16, 8, 0.1, ctypes.byref(p), f, None) == oa.EINVAL
+    assert L.omni_qwen3_attend(f, f, f, None, 0, f, f, 16, odd, 16, 8, 0.1, ctypes.byref(p), f, None) == oa.EINVAL
+    p8 = oa.decode_plan(4, 8, 8, 16, 1000, chunk=128)
+    assert L.omni_lm_attend_fp8(f, odd, f, None, 0, f, f, 16, f, 8, 0.1, 1000, ctypes.byref(p8), f, None) == oa.EINVAL
+    kvl = ctypes.c_void_p(4096)
+    for q, k, v, out in [(odd, f, f, f), (f, odd, f, f), (f, f, eight, f), (f, f, f, odd)]:
+        assert L.omni_hidream_attend(q, k, v, out, 10, kvl, 6144, 0, 0.1, 32, 8, None) == oa.EINVAL
+    assert L.omni_hidream_attend_batched(f, f, f, f, 10, kvl, 6144, 0, 0.1, 32, 8, 2, 61444, 0, 0, None) == oa.EINVAL
+    assert L.omni_hidream_attend_batched(f, f, f, f, 10, kvl, 6144, 0, 0.1, 32, 8, 2, 0, -8, 0, None) == oa.EINVAL
+    assert "batch strides" in L.omni_attn_last_error().decode()
+
+
+def test_prefill_rejects_bad_rows_and_plans():
+    L = oa.load()
+    plan = oa.PrefillPlan()
+    for seq, pos in [([0, -1], [0, 0]), ([0, 0], [2**31 - 2, 2**31 - 1])]:
+        s = np.array(seq, np.int32)
+        q = np.array(pos, np.int32)
+        rc = L.omni_attn_prefill_plan_init(2, 32, 8, 16, s.ctypes.data_as(ctypes.c_void_p),
+                                           q.ctypes.data_as(ctypes.c_void_p), None, 0, ctypes.byref(plan))
+        assert rc == oa.ETABLE, (seq, pos)
+    f, odd = ctypes.c_void_p(4096), ctypes.c_void_p(4098)
+    good, _, _ = _plan_host(4, 32, 8, np.zeros(4, np.int32), np.arange(4, dtype=np.int32))
+    bad = oa.PrefillPlan.from_buffer_copy(good)
+    bad.hk = 0
+    assert L.omni_attn_prefill_run(ctypes.byref(bad), f, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
+    bad = oa.PrefillPlan.from_buffer_copy(good)
+    bad.page = 12
+    assert L.omni_attn_prefill_run(ctypes.byref(bad), f, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
+    assert L.omni_attn_prefill_run(ctypes.byref(good), odd, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
+
+
+def test_rows_push_keeps_positions_and_slots_in_int32():
+    r = oa.Rows(page=16)
+    with pytest.raises(oa.OmniAttnError) as e:
+        r.push(np.arange(8), 2**31 - 4, 8, 0)  # positions past int32
+    assert e.value.code == oa.EINVAL
+    with pytest.raises(oa.OmniAttnError) as e:
+        r.push([2**31 // 16], 0, 4, 0)  # the page's slots pass int32
+    assert e.value.code == oa.ETABLE
+    r.push([2**31 // 16 - 1], 0, 16, 0)  # the last page that fits
+    assert int(r.slot[-1]) == 2**31 - 1
