@@ -196,6 +196,21 @@ def _i32_dev(t, name):
         raise OmniAttnError(EINVAL, f"{name} must be a contiguous int32 device tensor")
 
 
+def _ws(plan, workspace):
+    """The workspace pointer for a decode run, after checking that it holds the
+    plan's split partials (the C call takes no size: a smaller buffer would be
+    written past its end)."""
+    need = int(plan.workspace_bytes)
+    if workspace is None:
+        return None
+    if workspace.numel() * workspace.element_size() < need:
+        raise OmniAttnError(EWORKSPACE, f"workspace holds {workspace.numel() * workspace.element_size()} bytes, "
+                                        f"the plan needs {need}")
+    if not workspace.is_cuda or not workspace.is_contiguous():
+        raise OmniAttnError(EINVAL, "workspace must be a contiguous device tensor")
+    return _ptr(workspace)
+
+
 # --------------------------------------------------------------------- decode
 def decode_plan(rows: int, hq: int, hk: int, page: int, max_len: int, chunk: int = 0) -> DecodePlan:
     plan = DecodePlan()
@@ -235,7 +250,7 @@ def qwen3_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, out, hq, hk, sc
         _i32_dev(t, n)
     _check(load().omni_qwen3_attend(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr),
                                     _ptr(pages), page, _ptr(out), hq, hk, float(scale), ctypes.byref(plan),
-                                    _ptr(workspace), _stream(stream)))
+                                    _ws(plan, workspace), _stream(stream)))
     return out
 
 
@@ -259,8 +274,8 @@ def lm_attend(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, scale,
     for t, n in ((pos, "pos"), (seq, "seq"), (indptr, "indptr"), (pages, "pages")):
         _i32_dev(t, n)
     _check(load().omni_lm_attend(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr), _ptr(pages),
-                                 page, _ptr(out), heads, float(scale), context, ctypes.byref(plan), _ptr(workspace),
-                                 _stream(stream)))
+                                 page, _ptr(out), heads, float(scale), context, ctypes.byref(plan),
+                                 _ws(plan, workspace), _stream(stream)))
     return out
 
 
@@ -277,7 +292,7 @@ def lm_attend_fp8(qkv, kv, pos, seq, ragged, indptr, pages, page, out, heads, sc
         _i32_dev(t, n)
     _check(load().omni_lm_attend_fp8(_ptr(qkv), _ptr(kv), _ptr(pos), _ptr(seq), int(ragged), _ptr(indptr),
                                      _ptr(pages), page, _ptr(out), heads, float(scale), context, ctypes.byref(plan),
-                                     _ptr(workspace), _stream(stream)))
+                                     _ws(plan, workspace), _stream(stream)))
     return out
 
 
@@ -287,7 +302,7 @@ def decode_lastlen(qkv, kv, last_page_len, seq, ragged, indptr, pages, page, out
     _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
     _check(load().omni_attn_decode_run_lastlen(_ptr(qkv), _ptr(kv), _ptr(last_page_len), _ptr(seq), int(ragged),
                                                _ptr(indptr), _ptr(pages), page, _ptr(out), hq, hk, float(scale),
-                                               ctypes.byref(plan), _ptr(workspace), _stream(stream)))
+                                               ctypes.byref(plan), _ws(plan, workspace), _stream(stream)))
     return out
 
 
@@ -400,7 +415,7 @@ def qwen3_attend_dense(qkv, kv, per, base, span, out, hq, hk, scale, plan, works
     plan is made with page = 1 and max_len >= base + per."""
     _bf16_dev(qkv, "qkv"), _bf16_dev(kv, "kv"), _bf16_dev(out, "out")
     _check(load().omni_qwen3_attend_dense(_ptr(qkv), _ptr(kv), per, base, span, _ptr(out), hq, hk, float(scale),
-                                          ctypes.byref(plan), _ptr(workspace), _stream(stream)))
+                                          ctypes.byref(plan), _ws(plan, workspace), _stream(stream)))
     return out
 
 

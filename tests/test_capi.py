@@ -299,3 +299,13 @@ def test_rows_push_keeps_positions_and_slots_in_int32():
     assert e.value.code == oa.ETABLE
     r.push([2**31 // 16 - 1], 0, 16, 0)  # the last page that fits
     assert int(r.slot[-1]) == 2**31 - 1
+
+
+def test_python_wrappers_refuse_a_short_workspace():
+    """The C run takes no workspace size, so the binding checks it against
+    the plan before the call (a shorter buffer would be written past)."""
+    torch = pytest.importorskip("torch")
+    p = oa.decode_plan(4, 16, 8, 16, 1000, chunk=128)
+    with pytest.raises(oa.OmniAttnError) as e:
+        oa._ws(p, torch.empty(int(p.workspace_bytes) - 16, dtype=torch.uint8))
+    assert e.value.code == oa.EWORKSPACE and "the plan needs" in str(e.value)
