@@ -314,3 +314,26 @@ def test_prefill_long_sequence(oracle):
     sub = W.PagedCase(hq=32, hk=8, page=c.page, pos=c.pos[pick], seq=c.seq[pick], ragged=1, indptr=c.indptr,
                       pages=c.pages, num_pages=c.num_pages, qkv=c.qkv[pick], kv=c.kv)
     assert_close(got[pick], oracle_paged(oracle, sub), what="long prefill, first and last rows")
+
+
+def test_prefill_error_against_f64_truth_is_near_the_f32_p_kernels():
+    """The MFMA prefill rounds P to bf16 (an MFMA operand) where
+    qwen3_attend(ragged = 1) keeps it in f32 (qwen3.cu:123-208). Against f64
+    SDPA its error stays within 2.5x the mean and 2x the max of the split-K
+    decode kernel (f32 P) on the same rows."""
+    from refs import paged_truth
+    from gpu_util import bits_f32
+
+    c = W.ragged_prefill_case(2, 32, 8, 300, 700, 0, 200, seed=29)
+    pre = run_prefill(c)
+    plan = oa.decode_plan(c.rows, c.hq, c.hk, c.page, int(c.pos.max()) + 1)
+    out = torch.zeros(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    oa.qwen3_attend(dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), 1, dev_i32(c.indptr),
+                    dev_i32(c.pages), c.page, out, c.hq, c.hk, c.scale, plan, oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    truth = paged_truth(c).reshape(c.rows, -1)
+    e_pre = np.abs(bits_f32(pre).astype(np.float64) - truth)
+    e_dec = np.abs(bits_f32(host_bits(out)).astype(np.float64) - truth)
+    assert e_pre.mean() <= 2.5 * e_dec.mean(), (e_pre.mean(), e_dec.mean())
+    assert e_pre.max() <= 2.0 * e_dec.max(), (e_pre.max(), e_dec.max())
+    assert e_pre.max() < 2e-2 / 4 and e_pre.mean() < 2e-3 / 4
