@@ -1,5 +1,6 @@
 """Seeded random sweeps of every attention kernel against the CPU oracle:
 shapes, GQA ratios, page sizes, lengths, splits and modes drawn per case
+(ragged prefill rows also through the split-K decode kernel)
 from a generator seeded by the case number, so any failure names a case
 that reruns exactly. Sizes stay small enough for the oracle to finish in
 well under a second per case."""
@@ -13,7 +14,7 @@ from gpu_util import assert_close, dev_bits, dev_i32, host_bits
 
 pytestmark = pytest.mark.gpu
 
-CASES = range(16)
+CASES = range(24)
 
 
 def _paged_oracle(oracle, c):
@@ -90,7 +91,15 @@ def test_prefill_sweep(oracle, case):
     oa.prefill_run(pf, dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), dev_i32(c.indptr),
                    dev_i32(c.pages), out, c.scale)
     torch.cuda.synchronize()
-    assert_close(host_bits(out), _paged_oracle(oracle, c), what=what)
+    want = _paged_oracle(oracle, c)
+    assert_close(host_bits(out), want, what=what)
+    if hq // hk <= 4:  # the same ragged rows through the split-K decode kernel (qwen3_attend, ragged = 1)
+        plan = oa.decode_plan(c.rows, hq, hk, page, int(c.pos.max()) + 1, int(rng.choice([0, 128, 256])))
+        out2 = torch.zeros_like(out)
+        oa.qwen3_attend(dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), 1, dev_i32(c.indptr),
+                        dev_i32(c.pages), page, out2, hq, hk, c.scale, plan, oa.workspace_for(plan))
+        torch.cuda.synchronize()
+        assert_close(host_bits(out2), want, what=f"{what} (decode kernel, chunk {plan.chunk})")
 
 
 @pytest.mark.parametrize("case", CASES)
