@@ -90,9 +90,23 @@ __device__ __forceinline__ void merge_waves(const DecodeArgs& a, int n, int kh, 
 // workspace, slot (n / per) * span + t (qwen3_attend_dense).
 constexpr int kSlotsLane = 0, kSlotsUniform = 1, kSlotsDense = 2;
 
+// Split index of workgroup slot `slot` (0 .. S - 1) of unit u. Workgroup i runs
+// on XCD i % 8, and a unit's S slots are consecutive workgroups, so slot x of
+// unit u lands on XCD (x + S u) % 8, a phase with period P = 8 / gcd(S, 8) in u.
+// Slot x alone would pin each split index to a few XCDs (S = 2 or 4: the short
+// rows' absent last splits leave half the XCDs idle while the other half read
+// every first split). Rotating the slot by u / P pairs every phase with every
+// split index over P S consecutive units, so each XCD gets an even share of
+// each split index.
+__device__ __forceinline__ int rotated_split(int slot, int u, int S) {
+  const int P = 8 >> min(__builtin_ctz((unsigned)S), 3);
+  return (slot + u / P) % S;
+}
+
 template <int G, int SLOTS>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
-  const int split = blockIdx.x, kh = blockIdx.y, n = blockIdx.z;
+  const int kh = blockIdx.y, n = blockIdx.z;
+  const int split = rotated_split(blockIdx.x, kh + a.hk * n, a.splits);
   const int s = a.ragged ? a.seq[n] : n;
   const int len = decode_len(a, n, s);
   const int split_len = decode_split_len(a, len);
@@ -337,7 +351,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
   const int groups = a.hk / H;
   const int x = blockIdx.x & 7, rest = blockIdx.x >> 3;
   const int kg = rest % groups, unit = (rest / groups) * 8 + x;
-  const int n = unit / a.splits, split = unit % a.splits;
+  const int n = unit / a.splits, split = rotated_split(unit % a.splits, n, a.splits);
   if (n >= rows) return;
   const int s = a.ragged ? a.seq[n] : n;
   const int len = decode_len(a, n, s);
