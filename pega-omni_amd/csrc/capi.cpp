@@ -46,15 +46,16 @@ int log2i(int x) {
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 // Split size for a decode bucket: the largest chunk (<= 1024 keys) that
-// still gives the launch >= 2048 split workgroups at full length (8 per CU
-// on 256 CUs), down to 128. Measured on MI355X: a 128-session MHA tick
-// (4096 row x head pairs) runs best unsplit below 1024 keys, the 64-row
-// GQA talker (512 pairs) best at 512.
+// still gives the launch >= 4096 split workgroups at full length (16 per CU
+// on 256 CUs), down to 256. Measured on MI355X over seven bucket shapes: a
+// 128-session MHA tick (4096 row x head pairs) runs best at 1024, buckets of
+// 128-512 pairs best at 256-384 (the 64-row GQA talker: 59.5 us at 256
+// against 64.0 at 512), and 128-key splits were slower in every shape.
 int pick_chunk(int rows, int hk, int max_len) {
   int chunk = 1024;
-  while (chunk > 128) {
+  while (chunk > 256) {
     const long long units = (long long)rows * hk * (((long long)max_len + chunk - 1) / chunk);
-    if (units >= 2048) break;
+    if (units >= 4096) break;
     chunk /= 2;
   }
   return chunk;
