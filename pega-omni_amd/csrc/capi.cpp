@@ -386,11 +386,21 @@ int resident_tiled_groups() {
 
 }  // namespace
 
-int omni_hidream_attend_batched(const void* q, const void* k, const void* v, void* out, int q_len,
-                                const int32_t* kv_len_at, int q_stride, int causal, float scale_log2, int hq, int hk,
-                                int batch, int64_t q_bstride, int64_t kv_bstride, int64_t out_bstride, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Validation and argument packing shared by the DiT entry points. Returns
+// OMNI_ATTN_OK with `a` filled and `*empty` set when there is nothing to do.
+int dit_prepare(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
+                int q_stride, int causal, float scale_log2, int hq, int hk, int batch, int64_t q_bstride,
+                int64_t kv_bstride, int64_t out_bstride, omni::TiledArgs* a, bool* empty) {
+  *empty = false;
   if (q_len < 0 || batch < 0) return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_len=%d batch=%d", q_len, batch);
-  if (q_len == 0 || batch == 0) return ok();
+  if (q_len == 0 || batch == 0) {
+    *empty = true;
+    return ok();
+  }
   if (!q || !k || !v || !out || !kv_len_at) return fail(OMNI_ATTN_EINVAL, "hidream_attend: null device pointer");
   if (hk <= 0 || hq <= 0 || hq % hk != 0)
     return fail(OMNI_ATTN_EINVAL, "hidream_attend: hq=%d is not a multiple of hk=%d", hq, hk);
@@ -401,27 +411,47 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
     return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_stride=%d", q_stride);
   if (batch > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: batch=%d", batch);
   if (int rc = dit_alignment(q, k, v, out, batch, q_bstride, kv_bstride, out_bstride)) return rc;
-  omni::TiledArgs a{};
-  a.q = static_cast<const omni::bf16_t*>(q);
-  a.q_stride = q_stride;
-  a.k = static_cast<const omni::bf16_t*>(k);
-  a.v = static_cast<const omni::bf16_t*>(v);
-  a.kv_len_at = kv_len_at;
-  a.q_len = q_len;
-  a.causal = causal ? 1 : 0;
-  a.q_bstride = q_bstride;
-  a.kv_bstride = kv_bstride;
-  a.out_bstride = out_bstride;
-  a.out = static_cast<omni::bf16_t*>(out);
-  a.hq = hq;
-  a.hk = hk;
-  a.scale_log2 = scale_log2;
-  a.halved = omni::dit_halves(a, batch, resident_tiled_groups());
+  *a = omni::TiledArgs{};
+  a->q = static_cast<const omni::bf16_t*>(q);
+  a->q_stride = q_stride;
+  a->k = static_cast<const omni::bf16_t*>(k);
+  a->v = static_cast<const omni::bf16_t*>(v);
+  a->kv_len_at = kv_len_at;
+  a->q_len = q_len;
+  a->causal = causal ? 1 : 0;
+  a->q_bstride = q_bstride;
+  a->kv_bstride = kv_bstride;
+  a->out_bstride = out_bstride;
+  a->out = static_cast<omni::bf16_t*>(out);
+  a->hq = hq;
+  a->hk = hk;
+  a->scale_log2 = scale_log2;
+  return ok();
+}
+
+int dit_launch(const omni::TiledArgs& a, int batch, void* stream) {
   const int rc = omni::launch_dit(a, batch, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: shape not implemented");
   if (rc != 0)
     return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int omni_hidream_attend_batched(const void* q, const void* k, const void* v, void* out, int q_len,
+                                const int32_t* kv_len_at, int q_stride, int causal, float scale_log2, int hq, int hk,
+                                int batch, int64_t q_bstride, int64_t kv_bstride, int64_t out_bstride, void* stream) {
+  omni::TiledArgs a;
+  bool empty = false;
+  if (int rc = dit_prepare(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, batch, q_bstride,
+                           kv_bstride, out_bstride, &a, &empty))
+    return rc;
+  if (empty) return ok();
+  a.halved = omni::dit_halves(a, batch, resident_tiled_groups());
+  return dit_launch(a, batch, stream);
 }
 
 int64_t omni_hidream_workspace_bytes(void) { return (int64_t)resident_tiled_groups() * omni::kSegmentBytes; }
@@ -433,35 +463,14 @@ int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* ou
   if (!workspace)
     return omni_hidream_attend_batched(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, batch,
                                        q_bstride, kv_bstride, out_bstride, stream);
-  if (q_len < 0 || batch < 0) return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_len=%d batch=%d", q_len, batch);
-  if (q_len == 0 || batch == 0) return ok();
-  if (!q || !k || !v || !out || !kv_len_at) return fail(OMNI_ATTN_EINVAL, "hidream_attend: null device pointer");
-  if (hk <= 0 || hq <= 0 || hq % hk != 0)
-    return fail(OMNI_ATTN_EINVAL, "hidream_attend: hq=%d is not a multiple of hk=%d", hq, hk);
-  const int G = hq / hk;
-  if (G != 1 && G != 2 && G != 4 && G != 8)
-    return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: hq/hk=%d not in {1,2,4,8}", G);
-  if (q_stride < hq * OMNI_ATTN_HEAD_DIM || q_stride % 8 != 0)
-    return fail(OMNI_ATTN_EINVAL, "hidream_attend: q_stride=%d", q_stride);
-  if (batch > 65535) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: batch=%d", batch);
-  if (int rc = dit_alignment(q, k, v, out, batch, q_bstride, kv_bstride, out_bstride)) return rc;
+  omni::TiledArgs a;
+  bool empty = false;
+  if (int rc = dit_prepare(q, k, v, out, q_len, kv_len_at, q_stride, causal, scale_log2, hq, hk, batch, q_bstride,
+                           kv_bstride, out_bstride, &a, &empty))
+    return rc;
+  if (empty) return ok();
   if ((reinterpret_cast<uintptr_t>(workspace) & 15) != 0)
     return fail(OMNI_ATTN_EINVAL, "hidream_attend: workspace must be 16-byte aligned");
-  omni::TiledArgs a{};
-  a.q = static_cast<const omni::bf16_t*>(q);
-  a.q_stride = q_stride;
-  a.k = static_cast<const omni::bf16_t*>(k);
-  a.v = static_cast<const omni::bf16_t*>(v);
-  a.kv_len_at = kv_len_at;
-  a.q_len = q_len;
-  a.causal = causal ? 1 : 0;
-  a.q_bstride = q_bstride;
-  a.kv_bstride = kv_bstride;
-  a.out_bstride = out_bstride;
-  a.out = static_cast<omni::bf16_t*>(out);
-  a.hq = hq;
-  a.hk = hk;
-  a.scale_log2 = scale_log2;
   int items = 0;
   omni::dit_split(a, batch, resident_tiled_groups(), &items, &a.split_from, &a.split_k);
   const int64_t need = (int64_t)(items - a.split_from) * a.split_k * omni::kSegmentBytes;
@@ -469,11 +478,7 @@ int omni_hidream_attend_ws(const void* q, const void* k, const void* v, void* ou
     return fail(OMNI_ATTN_EWORKSPACE, "hidream_attend: the split needs %lld workspace bytes, got %lld",
                 (long long)need, (long long)workspace_bytes);
   a.ws = static_cast<float*>(workspace);
-  const int rc = omni::launch_dit(a, batch, as_stream(stream));
-  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "hidream_attend: shape not implemented");
-  if (rc != 0)
-    return fail(OMNI_ATTN_ELAUNCH, "hidream_attend: launch failed: %s", hipGetErrorString(omni::g_launch_status));
-  return ok();
+  return dit_launch(a, batch, stream);
 }
 
 int omni_hidream_attend(const void* q, const void* k, const void* v, void* out, int q_len, const int32_t* kv_len_at,
