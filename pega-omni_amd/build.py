@@ -31,13 +31,19 @@ FLAGS = [
 ]
 
 
+# Per-source additions. The decode kernels stream K/V and do little math:
+# LLVM's memory-clause scheduling strategy groups their loads, 0.1-0.3% faster
+# on every decode workload. The MFMA kernels were 1-3% slower under it.
+SOURCE_FLAGS = {"decode.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-x", "hip", "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(os.path.basename(src), []), "-x", "hip", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
