@@ -309,3 +309,23 @@ def test_python_wrappers_refuse_a_short_workspace():
     with pytest.raises(oa.OmniAttnError) as e:
         oa._ws(p, torch.empty(int(p.workspace_bytes) - 16, dtype=torch.uint8))
     assert e.value.code == oa.EWORKSPACE and "the plan needs" in str(e.value)
+
+
+def test_empty_batches_return_before_any_launch():
+    """A bucket with no rows (decode, prefill) is a no-op that returns OK on any
+    host, GPU or not: nothing is launched."""
+    L = oa.load()
+    f = ctypes.c_void_p(4096)
+    p = oa.decode_plan(0, 16, 8, 16, 1000)
+    assert p.rows == 0
+    assert L.omni_qwen3_attend(f, f, f, None, 0, f, f, 16, f, 16, 8, 0.1, ctypes.byref(p), f, None) == oa.OK
+    p8 = oa.decode_plan(0, 8, 8, 16, 1000)
+    assert L.omni_lm_attend_fp8(f, f, f, None, 0, f, f, 16, f, 8, 0.1, 1000, ctypes.byref(p8), f, None) == oa.OK
+    plan = oa.PrefillPlan()
+    rc = L.omni_attn_prefill_plan_init(0, 32, 8, 16, None, None, None, 0, ctypes.byref(plan))
+    assert rc == oa.EWORKSPACE and plan.work_bytes == 16 * 4  # the header alone
+    work = np.zeros(16, np.int32)
+    rc = L.omni_attn_prefill_plan_init(0, 32, 8, 16, None, None, work.ctypes.data_as(ctypes.c_void_p), 16,
+                                       ctypes.byref(plan))
+    assert rc == oa.OK and plan.tiles == 0
+    assert L.omni_attn_prefill_run(ctypes.byref(plan), f, f, f, f, f, f, f, 0.1, f, None) == oa.OK
