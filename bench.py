@@ -505,8 +505,30 @@ def short_bench(stream, steps, warmup):
     return res
 
 
+PEAKS_SRC = os.path.join(ROOT, "bench_peaks.hip")
+PEAKS_LIB = os.path.join(ROOT, "bench_peaks.so")
+
+
+def build_peaks():
+    """Compile the benchmark's peak probes (bench_peaks.hip) for gfx950 into
+    bench_peaks.so beside this file. They are measurement code, kept out of
+    the attention library's build."""
+    import subprocess
+
+    sys.path.insert(0, os.path.join(ROOT, "pega-omni_amd"))
+    import build as hip_build
+
+    tmp = PEAKS_LIB + ".tmp"
+    r = subprocess.run([hip_build.HIPCC, *hip_build.FLAGS, "-x", "hip", "-shared", PEAKS_SRC, "-o", tmp],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {PEAKS_SRC}:\n{r.stderr}")
+    os.replace(tmp, PEAKS_LIB)
+    return PEAKS_LIB
+
+
 def measure_peaks(stream):
-    """Measured ceilings on this GPU (libomni_peaks.so): bf16 MFMA TFLOP/s
+    """Measured ceilings on this GPU (bench_peaks.so): bf16 MFMA TFLOP/s
     (4 independent 32x32x16 chains per wave) on smooth operands and on random
     ones (the clock drops as more operand bits toggle; random data is what
     attention feeds the MFMAs), v_exp_f32 and v_fma_f32 lane
@@ -515,7 +537,10 @@ def measure_peaks(stream):
 
     import torch
 
-    L = ctypes.CDLL(os.path.join(ROOT, "pega-omni_amd", "libomni_peaks.so"))
+    if not os.path.exists(PEAKS_LIB):
+        log("[bench] bench_peaks.so is not built: building it")
+        build_peaks()
+    L = ctypes.CDLL(PEAKS_LIB)
     P, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     L.omni_peaks_mfma.argtypes = [P, i32, i32, i32, P]
     L.omni_peaks_valu.argtypes = [P, i32, i32, i32, P]
@@ -683,6 +708,7 @@ def main():
     ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
+    ap.add_argument("--build-peaks", action="store_true", help="compile bench_peaks.hip into bench_peaks.so and exit")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 CSV output directories (with --kernel, --last) and exit")
     ap.add_argument("--kernel", nargs="+", default=["tiled_attn"],
@@ -691,6 +717,9 @@ def main():
     ap.add_argument("--flops", type=float, default=None, help="algorithmic flops per call (--summarize)")
     ap.add_argument("--bytes", type=float, default=None, help="algorithmic bytes per call (--summarize)")
     args = ap.parse_args()
+    if args.build_peaks:
+        print(f"built {build_peaks()}")
+        return
     if args.summarize:
         summarize_profile(args.summarize, args.kernel, args.last, args.flops, nbytes=args.bytes)
         return

@@ -1,7 +1,9 @@
 // Peak microbenchmarks for gfx950, used by bench.py to report the measured
 // ceilings next to the published ones: bf16 MFMA throughput, v_exp_f32 and
-// v_fma_f32 issue rates, and streaming HBM read bandwidth. Built into
-// libomni_peaks.so, separate from the attention library.
+// v_fma_f32 issue rates, and streaming HBM read bandwidth. A measurement
+// probe of the benchmark, not part of the attention library: built into
+// bench_peaks.so by `python bench.py --build-peaks` (bench.py builds it on
+// first use when it is missing).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

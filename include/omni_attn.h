@@ -54,7 +54,7 @@ typedef struct omni_attn_decode_plan {
   int32_t rows;     /* rows per launch (the batch bucket) */
   int32_t hq, hk;   /* query heads, K/V heads (hq % hk == 0, hq / hk in {1,2,4}, as the
                        reference's stack.rs:94-106 accepts) */
-  int32_t page;     /* tokens per page, a power of two */
+  int32_t page;     /* tokens per page, any positive size (16 in every engine) */
   int32_t max_len;  /* bound on keys any row sees; longer rows still run, slower */
   int32_t chunk;    /* keys per split (a multiple of 128) */
   int32_t splits;   /* ceil(max_len / chunk): workgroups per (row, kv head) */

@@ -15,8 +15,6 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libomni_attn.so")
-PEAKS_SRC = os.path.join(HERE, "probe", "peaks.hip")
-PEAKS_OUT = os.path.join(HERE, "libomni_peaks.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -60,14 +58,8 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, OUT)
-    # The peak microbenchmarks bench.py reports beside the published peaks.
-    r = subprocess.run([HIPCC, *FLAGS, "-x", "hip", "-shared", PEAKS_SRC, "-o", PEAKS_OUT + ".tmp"],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {PEAKS_SRC}:\n{r.stderr}")
-    os.replace(PEAKS_OUT + ".tmp", PEAKS_OUT)
     if verbose:
-        print(f"built {OUT} and {PEAKS_OUT}")
+        print(f"built {OUT}")
     return OUT
 
 

@@ -36,13 +36,6 @@ int ok() {
   return OMNI_ATTN_OK;
 }
 
-bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
-int log2i(int x) {
-  int s = 0;
-  while ((1 << s) < x) ++s;
-  return s;
-}
-
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 // Split size for a decode bucket: the largest chunk (<= 1024 keys) that
@@ -106,7 +99,7 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.hq = hq;
   a.hk = hk;
   a.ragged = ragged ? 1 : 0;
-  a.page_shift = log2i(page);
+  a.pd = omni::make_page_div(page);
   a.context = context > 0 ? context : INT_MAX;
   a.len_mode = len_mode;
   a.chunk = plan->chunk;
@@ -141,7 +134,7 @@ int omni_attn_decode_plan_init(int rows, int hq, int hk, int page, int max_len, 
     return fail(OMNI_ATTN_EINVAL, "decode_plan: hq=%d is not a multiple of hk=%d", hq, hk);
   const int G = hq / hk;
   if (G != 1 && G != 2 && G != 4) return fail(OMNI_ATTN_EUNSUPPORTED, "decode_plan: hq/hk=%d not in {1,2,4}", G);
-  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "decode_plan: page=%d is not a power of two", page);
+  if (page <= 0) return fail(OMNI_ATTN_EINVAL, "decode_plan: page=%d", page);
   if (max_len <= 0) return fail(OMNI_ATTN_EINVAL, "decode_plan: max_len=%d", max_len);
   int chunk = chunk_hint > 0 ? chunk_hint : pick_chunk(rows, hk, max_len);
   if (chunk % 128 != 0) return fail(OMNI_ATTN_EINVAL, "decode_plan: chunk=%d is not a multiple of 128", chunk);
@@ -241,8 +234,8 @@ int omni_attn_gather_kv(const void* kv, int hk, const int32_t* indptr, const int
   if (nseq == 0) return ok();
   if (!kv || !indptr || !pages || !seq_ids || !lens || !out_indptr || !out)
     return fail(OMNI_ATTN_EINVAL, "gather_kv: null device pointer");
-  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "gather_kv: page=%d is not a power of two", page);
-  if (omni::launch_gather_kv(kv, hk, indptr, pages, log2i(page), seq_ids, lens, out_indptr, nseq, out,
+  if (page <= 0) return fail(OMNI_ATTN_EINVAL, "gather_kv: page=%d", page);
+  if (omni::launch_gather_kv(kv, hk, indptr, pages, omni::make_page_div(page), seq_ids, lens, out_indptr, nseq, out,
                              as_stream(stream)) != 0)
     return fail(OMNI_ATTN_ELAUNCH, "gather_kv: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
@@ -259,7 +252,7 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   const int G = hq / hk;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: hq/hk=%d not in {1,2,4,8}", G);
-  if (!pow2(page)) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_plan: page=%d is not a power of two", page);
+  if (page <= 0) return fail(OMNI_ATTN_EINVAL, "prefill_plan: page=%d", page);
   if (rows > 0 && (!seq_h || !pos_h)) return fail(OMNI_ATTN_EINVAL, "prefill_plan: null host arrays");
   const int per_tile = omni::kTiledRows / G;  // query positions per tile
   plan->rows = rows;
@@ -330,10 +323,17 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
                           const int32_t* seq, const int32_t* indptr, const int32_t* pages, void* out, float scale,
                           const int32_t* work, void* stream) {
   if (!plan) return fail(OMNI_ATTN_EINVAL, "prefill_run: null plan");
-  if (plan->tiles < 0 || plan->workgroups < 0 || plan->hk <= 0 || plan->hq <= 0 || plan->hq % plan->hk != 0 ||
-      !pow2(plan->page))
-    return fail(OMNI_ATTN_EINVAL, "prefill_run: plan is not one prefill_plan_init made (tiles=%d hq=%d hk=%d page=%d)",
-                plan->tiles, plan->hq, plan->hk, plan->page);
+  // The kernel's grid and item ranges come from the plan and the work list:
+  // a plan whose fields disagree with each other would skip items silently.
+  const int G = plan->hk > 0 && plan->hq > 0 && plan->hq % plan->hk == 0 ? plan->hq / plan->hk : 0;
+  const int64_t items = (int64_t)plan->tiles * (plan->hk > 0 ? plan->hk : 0);
+  if (plan->tiles < 0 || (G != 1 && G != 2 && G != 4 && G != 8) || plan->page <= 0 ||
+      plan->tile_rows != omni::kTiledRows || plan->workgroups != (items + omni::kXcds - 1) / omni::kXcds * omni::kXcds ||
+      plan->work_bytes != (omni::kPrefillWorkHeader + 4 * items) * (int64_t)sizeof(int32_t))
+    return fail(OMNI_ATTN_EINVAL,
+                "prefill_run: plan is not one prefill_plan_init made (tiles=%d hq=%d hk=%d page=%d tile_rows=%d "
+                "workgroups=%d)",
+                plan->tiles, plan->hq, plan->hk, plan->page, plan->tile_rows, plan->workgroups);
   if (plan->tiles == 0) return ok();
   if (!qkv || !kv || !pos || !seq || !indptr || !pages || !out || !work)
     return fail(OMNI_ATTN_EINVAL, "prefill_run: null device pointer");
@@ -348,7 +348,7 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
   a.indptr = indptr;
   a.pages = pages;
   a.work = work;
-  a.page_shift = log2i(plan->page);
+  a.pd = omni::make_page_div(plan->page);
   a.causal = 1;
   a.out = static_cast<omni::bf16_t*>(out);
   a.hq = plan->hq;
@@ -714,8 +714,8 @@ struct omni_attn_rows {
 };
 
 omni_attn_rows* omni_attn_rows_new(int page, int ring) {
-  if (!pow2(page) || ring < 0) {
-    fail(OMNI_ATTN_EINVAL, "rows_new: page=%d (a power of two) ring=%d", page, ring);
+  if (page <= 0 || ring < 0) {
+    fail(OMNI_ATTN_EINVAL, "rows_new: page=%d ring=%d", page, ring);
     return nullptr;
   }
   omni_attn_rows* r = new (std::nothrow) omni_attn_rows();

@@ -37,7 +37,7 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int n, int s) {
   if (a.len_mode == 0)
     len = a.pos[n] + 1;
   else if (a.len_mode == 1)
-    len = ((a.indptr[s + 1] - a.indptr[s] - 1) << a.page_shift) + a.pos[s];
+    len = (a.indptr[s + 1] - a.indptr[s] - 1) * a.pd.page + a.pos[s];
   else
     len = a.dense_base + n % a.dense_per + 1;
   return min(len, a.context);
@@ -46,7 +46,7 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int n, int s) {
 // Keys per split of a row of `len` keys: ceil(len / chunk) splits (at most
 // the plan's), of equal length rounded up to 32 keys, so no split is a short
 // remainder. A multiple of 32 keeps every key group a kernel loads inside one
-// page when page >= the group.
+// page when the page is a multiple of the group.
 __device__ __forceinline__ int decode_split_len(const DecodeArgs& a, int len) {
   const int ns = len <= a.chunk ? 1 : min(a.splits, (len + a.chunk - 1) / a.chunk);
   return ((len + ns - 1) / ns + 31) & ~31;
@@ -85,25 +85,23 @@ __device__ __forceinline__ void merge_waves(const DecodeArgs& a, int n, int kh, 
 }
 
 // Where key t of a row lives. kSlotsUniform: every group of 4 key rows
-// (page >= 4) lies in one page, so its page id is one wave-uniform scalar
-// load; kSlotsLane: each lane loads its own page id; kSlotsDense: a dense
-// workspace, slot (n / per) * span + t (qwen3_attend_dense).
+// (page a multiple of 4) lies in one page, so its page id is one wave-uniform
+// scalar load; kSlotsLane: each lane loads its own page id; kSlotsDense: a
+// dense workspace, slot (n / per) * span + t (qwen3_attend_dense).
 constexpr int kSlotsLane = 0, kSlotsUniform = 1, kSlotsDense = 2;
 
-// Split index of workgroup slot `slot` (0 .. S - 1) of unit u. Workgroup i runs
-// on XCD i % 8, and a unit's S slots are consecutive workgroups, so slot x of
-// unit u lands on XCD (x + S u) % 8, a phase with period P = 8 / gcd(S, 8) in u.
-// Slot x alone would pin each split index to a few XCDs (S = 2 or 4: the short
-// rows' absent last splits leave half the XCDs idle while the other half read
-// every first split). Rotating the slot by u / P pairs every phase with every
-// split index over P S consecutive units, so each XCD gets an even share of
-// each split index.
-__device__ __forceinline__ int rotated_split(int slot, int u, int S) {
-  const int P = 8 >> min(__builtin_ctz((unsigned)S), 3);
-  return (slot + u / P) % S;
+// Page index and slot of token t. A power-of-two page (every engine's 16)
+// takes a shift and a mask; DIV: any other page, a multiply-high division.
+template <bool DIV>
+__device__ __forceinline__ int key_page(const PageDiv& d, int t) {
+  return DIV ? page_index(d, t) : t >> d.shift;
+}
+template <bool DIV>
+__device__ __forceinline__ int64_t key_slot(const PageDiv& d, int pid, int t) {
+  return DIV ? page_slot(d, pid, t) : (((int64_t)pid << d.shift) | (t & ((1 << d.shift) - 1)));
 }
 
-template <int G, int SLOTS>
+template <int G, int SLOTS, bool DIV>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int kh = blockIdx.y, n = blockIdx.z;
   const int split = rotated_split(blockIdx.x, kh + a.hk * n, a.splits);
@@ -133,7 +131,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int64_t per_slot = 2LL * a.hk * kHead;
   const bf16_t* kb = a.kv + (int64_t)kh * kHead + c * 8;
   const bf16_t* vb = a.kv + (int64_t)(a.hk + kh) * kHead + c * 8;
-  const int shift = a.page_shift, pmask = (1 << shift) - 1;
 
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -151,9 +148,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
     if constexpr (SLOTS == kSlotsDense)
       return 0;
     else if constexpr (SLOTS == kSlotsUniform)
-      return pg[__builtin_amdgcn_readfirstlane(min(tb + 4 * i, t1 - 1) >> shift)];
+      return pg[key_page<DIV>(a.pd, __builtin_amdgcn_readfirstlane(min(tb + 4 * i, t1 - 1)))];
     else
-      return pg[min(tb + 4 * i + r, t1 - 1) >> shift];
+      return pg[key_page<DIV>(a.pd, min(tb + 4 * i + r, t1 - 1))];
   };
   constexpr int kStride = kDecodeWaves * kTileKeys;
   // G = 1: two register tiles, the next tile's loads (and the page ids of the
@@ -171,7 +168,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
       if constexpr (SLOTS == kSlotsDense)
         off[i] = (dense_first + t) * per_slot;
       else
-        off[i] = (((int64_t)pid[i] << shift) | (t & pmask)) * per_slot;
+        off[i] = key_slot<DIV>(a.pd, pid[i], t) * per_slot;
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) x.kr[i] = ldg16_stream(kb + off[i]);
@@ -341,8 +338,9 @@ __device__ __forceinline__ float across_key_rows(float v) {
 }
 
 // NI load instructions (NI * R keys) per wave and iteration. UP: the R keys of
-// one instruction share a page (page >= R), so its id is a scalar load.
-template <int H, int NI, bool UP>
+// one instruction share a page (page a multiple of R), so its id is a scalar
+// load.
+template <int H, int NI, bool UP, bool DIV>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a, int rows) {
   constexpr int R = 8 / H;
   // Workgroup i runs on XCD i % 8: the head groups of one (row, split) unit
@@ -380,7 +378,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
   const int64_t sb = a.slot_bytes;
   const int64_t koff = (int64_t)kh * kHead + c * 16, voff = (int64_t)(a.hk + kh) * kHead + c * 16;
   const int64_t ksoff = 2LL * a.hk * kHead + kh * 4, vsoff = 2LL * a.hk * kHead + (a.hk + kh) * 4;
-  const int shift = a.page_shift, pmask = (1 << shift) - 1;
 
   float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
@@ -395,9 +392,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
   // plain in-order count.
   auto page_of = [&](int tb, int i) -> int {
     if constexpr (UP)
-      return pg[__builtin_amdgcn_readfirstlane(min(tb + R * i, t1 - 1) >> shift)];
+      return pg[key_page<DIV>(a.pd, __builtin_amdgcn_readfirstlane(min(tb + R * i, t1 - 1)))];
     else
-      return pg[min(tb + R * i + r, t1 - 1) >> shift];
+      return pg[key_page<DIV>(a.pd, min(tb + R * i + r, t1 - 1))];
   };
   struct Tile {
     uint4 kr[NI], vr[NI];
@@ -407,7 +404,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int t = min(tb + R * i + r, t1 - 1);
-      const uint8_t* sp = kvb + (((int64_t)pid[i] << shift) | (t & pmask)) * sb;
+      const uint8_t* sp = kvb + key_slot<DIV>(a.pd, pid[i], t) * sb;
       x.kr[i] = ldg16_stream(sp + koff);
       x.vr[i] = ldg16_stream(sp + voff);
       x.ks[i] = *reinterpret_cast<const float*>(sp + ksoff);
@@ -556,10 +553,17 @@ static void launch_fp8_h(const DecodeArgs& a, int rows, hipStream_t stream) {
   const int units = rows * a.splits;
   const dim3 grid(8 * (a.hk / H) * ((units + 7) / 8));
   constexpr int R = 8 / H;
-  if (a.page_shift >= __builtin_ctz(R))
-    decode_split_fp8<H, 4, true><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
-  else
-    decode_split_fp8<H, 4, false><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
+  const bool up = a.pd.page % R == 0;
+  if (!page_pow2(a.pd)) {
+    if (up)
+      decode_split_fp8<H, 4, true, true><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
+    else
+      decode_split_fp8<H, 4, false, true><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
+  } else if (up) {
+    decode_split_fp8<H, 4, true, false><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
+  } else {
+    decode_split_fp8<H, 4, false, false><<<grid, kDecodeThreads, 0, stream>>>(a, rows);
+  }
 }
 
 static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) {
@@ -582,11 +586,14 @@ static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   const dim3 grid(a.splits, a.hk, rows);
   if (a.fp8) return launch_decode_fp8(a, rows, stream);
-  const int slots = a.len_mode == 2 ? kSlotsDense : a.page_shift >= 2 ? kSlotsUniform : kSlotsLane;
-#define OMNI_DECODE(K, G)                                                                  \
-  (slots == kSlotsDense     ? K<G, kSlotsDense><<<grid, kDecodeThreads, 0, stream>>>(a)    \
-   : slots == kSlotsUniform ? K<G, kSlotsUniform><<<grid, kDecodeThreads, 0, stream>>>(a)  \
-                            : K<G, kSlotsLane><<<grid, kDecodeThreads, 0, stream>>>(a))
+  const int slots = a.len_mode == 2 ? kSlotsDense : a.pd.page % 4 == 0 ? kSlotsUniform : kSlotsLane;
+  const bool div = !page_pow2(a.pd);
+#define OMNI_DECODE(K, G)                                                                              \
+  (slots == kSlotsDense   ? K<G, kSlotsDense, false><<<grid, kDecodeThreads, 0, stream>>>(a)           \
+   : div && slots == kSlotsUniform ? K<G, kSlotsUniform, true><<<grid, kDecodeThreads, 0, stream>>>(a) \
+   : div                           ? K<G, kSlotsLane, true><<<grid, kDecodeThreads, 0, stream>>>(a)    \
+   : slots == kSlotsUniform        ? K<G, kSlotsUniform, false><<<grid, kDecodeThreads, 0, stream>>>(a) \
+                                   : K<G, kSlotsLane, false><<<grid, kDecodeThreads, 0, stream>>>(a))
   switch (a.hq / a.hk) {
     case 1: OMNI_DECODE(decode_split, 1); break;
     case 2: OMNI_DECODE(decode_split, 2); break;
@@ -625,8 +632,16 @@ int noalloc_scratch(float** ptr) {
   }
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[dev]) {
+    // The first call on a device may come while the caller's stream is being
+    // captured into a graph. The lookup is no stream work, but it may load
+    // this library's code object onto the device, which a capture in global
+    // mode refuses; relaxed mode for this thread, for the lookup only,
+    // admits it without touching the capture.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t mrc = hipThreadExchangeStreamCaptureMode(&mode);
     void* p = nullptr;
     const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (mrc == hipSuccess) hipThreadExchangeStreamCaptureMode(&mode);
     if (rc != hipSuccess || !p) {
       g_launch_status = rc;
       return -1;
@@ -642,27 +657,26 @@ int noalloc_scratch(float** ptr) {
 // Block per sequence i: copy its first lens[i] tokens' slots to dense rows.
 // Each slot is 2 * hk * 256 bytes, copied as 16-byte words.
 __global__ __launch_bounds__(256) void gather_kv_kernel(const uint4* kv, int hk, const int32_t* indptr,
-                                                        const int32_t* pages, int shift, const int32_t* seq_ids,
+                                                        const int32_t* pages, PageDiv pd, const int32_t* seq_ids,
                                                         const int32_t* lens, const int32_t* out_indptr, uint4* out) {
   const int i = blockIdx.x;
   const int s = seq_ids[i], len = lens[i];
   const int64_t words = 2LL * hk * kHead * 2 / 16;
   const int32_t* pg = pages + indptr[s];
-  const int pmask = (1 << shift) - 1;
   uint4* dst = out + (int64_t)out_indptr[i] * words;
   const int64_t total = (int64_t)len * words;
   for (int64_t w = blockIdx.y * 256 + threadIdx.x; w < total; w += (int64_t)gridDim.y * 256) {
     const int t = (int)(w / words);
-    const int64_t slot = ((int64_t)pg[t >> shift] << shift) | (t & pmask);
+    const int64_t slot = page_slot(pd, pg[page_index(pd, t)], t);
     dst[w] = kv[slot * words + (w % words)];
   }
 }
 
-int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int shift,
+int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, PageDiv pd,
                      const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
                      hipStream_t stream) {
   if (nseq == 0) return 0;
-  gather_kv_kernel<<<dim3(nseq, 16), 256, 0, stream>>>(static_cast<const uint4*>(kv), hk, indptr, pages, shift,
+  gather_kv_kernel<<<dim3(nseq, 16), 256, 0, stream>>>(static_cast<const uint4*>(kv), hk, indptr, pages, pd,
                                                       seq_ids, lens, out_indptr, static_cast<uint4*>(out));
   return check_launch();
 }

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "indexing.h"
+
 namespace omni {
 
 typedef uint16_t bf16_t;
@@ -28,7 +30,7 @@ struct DecodeArgs {
   float* ws_lse; // [rows][hq][splits] split log2-sum-exp
   int hq, hk;
   int ragged;
-  int page_shift;
+  PageDiv pd;   // page size and its divisor
   int context;  // cap on keys per row
   int len_mode;
   int chunk, splits;
@@ -49,7 +51,7 @@ constexpr int kMaxDevices = 64;
 // device); 0 on success, -1 if the lookup fails.
 int noalloc_scratch(float** ptr);
 
-int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, int shift,
+int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, PageDiv pd,
                      const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
                      hipStream_t stream);
 
@@ -64,7 +66,7 @@ struct TiledArgs {
   const int32_t* indptr;
   const int32_t* pages;
   const int32_t* work;  // 4 int32 per tile: seq, first row, rows, unused
-  int page_shift;
+  PageDiv pd;
   // dense source (mode 1): k, v [slots][hk][128]
   const bf16_t* k;
   const bf16_t* v;

@@ -265,10 +265,11 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   // Dense sources: within a full tile a lane's rows and chunks are fixed, so
   // its element offsets from the tile's first key are constants (32-bit) and a
   // tile adds one uniform base: loads take a scalar base and a vector offset.
-  // Paged sources with page >= kRowsPerWave: a wave's rows of a tile are
-  // consecutive keys of one page, so a tile needs one (scalar) page id per
-  // wave, read a tile ahead, and the rows are consecutive slots.
-  const bool page_wave = PAGED && (1 << a.page_shift) >= kRowsPerWave;
+  // Paged sources with a page that is a multiple of kRowsPerWave: a wave's
+  // rows of a tile are consecutive keys of one page, so a tile needs one
+  // (scalar) page id per wave, read a tile ahead, and the rows are
+  // consecutive slots.
+  const bool page_wave = PAGED && a.pd.page % kRowsPerWave == 0;
   // Element offsets of this lane's rows from the first row of the wave's
   // block (dense: from the tile's first key): constants for every tile.
   uint32_t koff[kRowsPerWave / 4], voff[kRowsPerWave / 4];
@@ -292,7 +293,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   const __amdgpu_buffer_rsrc_t pg_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(PAGED ? (void*)t.pg : nullptr, 0, -1, kBufferFlags);
   auto wave_page = [&](int n) -> int {
-    const int i = __builtin_amdgcn_readfirstlane(min(n + kRowsPerWave * wave_u, t.last - 1) >> a.page_shift);
+    const int i = page_index(a.pd, __builtin_amdgcn_readfirstlane(min(n + kRowsPerWave * wave_u, t.last - 1)));
     return __builtin_amdgcn_raw_buffer_load_b32(pg_rsrc, 0, 4 * i, 0);
   };
   int next_pid = 0;  // page id for the next tile to issue (page_wave), per lane
@@ -309,9 +310,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
       const int64_t stride_bytes = 2 * (PAGED ? t.per_slot : t.kv_stride);
       const int bytes = rows == (PAGED ? kRowsPerWave : kBN) ? -1 : (int)(rows * stride_bytes);
       if constexpr (PAGED) {
-        const int sh = a.page_shift;
-        const int64_t slot0 = ((int64_t)__builtin_amdgcn_readfirstlane(next_pid) << sh) |
-                              ((n0 + kRowsPerWave * wave_u) & ((1 << sh) - 1));
+        const int64_t slot0 = page_slot(a.pd, __builtin_amdgcn_readfirstlane(next_pid), n0 + kRowsPerWave * wave_u);
         kb = t.kbase + slot0 * t.per_slot;
         vb = t.vbase + slot0 * t.per_slot;
       } else {
@@ -340,8 +339,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
       const int vc = (((cs >> 2) ^ (row & 3)) << 2) | (cs & 3);
       int64_t off;
       if constexpr (PAGED) {
-        const int sh = a.page_shift;
-        off = (((int64_t)t.pg[key >> sh] << sh) | (key & ((1 << sh) - 1))) * t.per_slot;
+        off = page_slot(a.pd, t.pg[page_index(a.pd, key)], key) * t.per_slot;
       } else {
         off = (int64_t)key * t.kv_stride;
       }

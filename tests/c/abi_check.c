@@ -53,7 +53,8 @@ static void check_decode_plan(void) {
   /* documented rejections */
   CHECK(omni_attn_decode_plan_init(4, 16, 6, 16, 100, 0, &p) == OMNI_ATTN_EINVAL);        /* hq % hk */
   CHECK(omni_attn_decode_plan_init(4, 16, 2, 16, 100, 0, &p) == OMNI_ATTN_EUNSUPPORTED);  /* G = 8 */
-  CHECK(omni_attn_decode_plan_init(4, 16, 8, 12, 100, 0, &p) == OMNI_ATTN_EUNSUPPORTED);  /* page */
+  CHECK(omni_attn_decode_plan_init(4, 16, 8, 0, 100, 0, &p) == OMNI_ATTN_EINVAL);         /* page */
+  CHECK(omni_attn_decode_plan_init(4, 16, 8, 12, 100, 0, &p) == OMNI_ATTN_OK && p.page == 12); /* any page > 0 */
   CHECK(omni_attn_decode_plan_init(4, 16, 8, 16, 0, 0, &p) == OMNI_ATTN_EINVAL);          /* max_len */
   CHECK(omni_attn_decode_plan_init(4, 16, 8, 16, 100, 100, &p) == OMNI_ATTN_EINVAL);      /* chunk */
   CHECK(omni_attn_decode_plan_init(70000, 16, 8, 16, 100, 0, &p) == OMNI_ATTN_EINVAL);    /* rows */
@@ -177,7 +178,7 @@ static void check_prefill_plan(void) {
   free(work);
   /* rejections */
   CHECK(omni_attn_prefill_plan_init(4, 48, 3, 16, seq, pos, NULL, 0, &p) == OMNI_ATTN_EUNSUPPORTED); /* G = 16 */
-  CHECK(omni_attn_prefill_plan_init(4, 32, 8, 24, seq, pos, NULL, 0, &p) == OMNI_ATTN_EUNSUPPORTED); /* page */
+  CHECK(omni_attn_prefill_plan_init(4, 32, 8, 0, seq, pos, NULL, 0, &p) == OMNI_ATTN_EINVAL); /* page */
   CHECK(omni_attn_prefill_plan_init(4, 32, 8, 16, NULL, pos, NULL, 0, &p) == OMNI_ATTN_EINVAL);
   const int32_t neg[2] = {-1, 0}, s2[2] = {0, 0};
   CHECK(omni_attn_prefill_plan_init(2, 32, 8, 16, s2, neg, NULL, 0, &p) == OMNI_ATTN_ETABLE);
@@ -232,7 +233,13 @@ static void check_rows(void) {
   CHECK(omni_attn_rows_push(g, lease_a, 3, 45, 1, 0) == OMNI_ATTN_OK);
   CHECK(omni_attn_rows_get(g, OMNI_ATTN_ROWS_SLOT)[0] == 9 * 16 + 5);
   omni_attn_rows_free(g);
-  CHECK(omni_attn_rows_new(12, 0) == NULL);
+  CHECK(omni_attn_rows_new(0, 0) == NULL);
+  /* any positive page: slot of position p is lease[p / page] * page + p % page */
+  omni_attn_rows* t12 = omni_attn_rows_new(12, 0);
+  CHECK(t12 != NULL);
+  CHECK(omni_attn_rows_push(t12, lease_a, 3, 25, 1, 0) == OMNI_ATTN_OK);
+  CHECK(omni_attn_rows_get(t12, OMNI_ATTN_ROWS_SLOT)[0] == lease_a[2] * 12 + 1);
+  omni_attn_rows_free(t12);
   CHECK(omni_attn_rows_new(16, -1) == NULL);
 }
 
@@ -259,8 +266,7 @@ static void check_head64_validation(void) {
         OMNI_ATTN_EINVAL);
   CHECK(omni_hidream_qk_rope(kFake, 48 * 128, kFake, kFake, kFake, kFake, kFake, kFake, 4, 32, 8, 22, 1e-6f, 5e6f,
                              NULL) == OMNI_ATTN_EINVAL);
-  CHECK(omni_attn_gather_kv(kFake, 8, kFake, kFake, 12, kFake, kFake, kFake, 2, kFake, NULL) ==
-        OMNI_ATTN_EUNSUPPORTED);
+  CHECK(omni_attn_gather_kv(kFake, 8, kFake, kFake, 0, kFake, kFake, kFake, 2, kFake, NULL) == OMNI_ATTN_EINVAL);
 }
 
 int main(void) {

@@ -6,6 +6,7 @@
   before it launches;
 * the same program and tests/c/host_fuzz.c (seeded malformed inputs) against
   a build of capi.cpp's host pass under AddressSanitizer + UBSan;
+* the kernels' index arithmetic (csrc/indexing.h) on the host (tests/c/indexing_check.cpp);
 * the ctypes signatures the Python mirror binds agree, parameter by
   parameter, with the prototypes the header declares.
 """
@@ -33,6 +34,14 @@ def test_abi_check_c_consumer():
         pytest.skip("libomni_attn.so is not built")
     out = _make("abi")
     assert "checks passed" in out
+
+
+def test_kernel_index_arithmetic_on_the_host():
+    """A host build of csrc/indexing.h: the kernels' multiply-high division by
+    any page size against / and %, and the decode split rotation (every split
+    index of a unit exactly once, for 1..64 splits and many units)."""
+    out = _make("indexing")
+    assert "page division" in out and "split rotation" in out
 
 
 @pytest.mark.skipif(os.environ.get("OMNI_SANITIZED") == "1", reason="already running under the sanitizer build")

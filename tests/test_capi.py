@@ -44,7 +44,8 @@ def test_decode_plan_shapes():
 @pytest.mark.parametrize("args,code", [
     ((4, 16, 6, 16, 100, 0), oa.EINVAL),        # hq not a multiple of hk
     ((4, 16, 2, 16, 100, 0), oa.EUNSUPPORTED),  # G = 8 not implemented in decode
-    ((4, 16, 8, 12, 100, 0), oa.EUNSUPPORTED),  # page not a power of two
+    ((4, 16, 8, 0, 100, 0), oa.EINVAL),         # page not positive
+    ((4, 16, 8, -16, 100, 0), oa.EINVAL),       # page not positive
     ((4, 16, 8, 16, 0, 0), oa.EINVAL),          # max_len
     ((4, 16, 8, 16, 100, 100), oa.EINVAL),      # chunk not a multiple of 128
     ((70000, 16, 8, 16, 100, 0), oa.EINVAL),    # rows beyond grid limit
@@ -283,9 +284,15 @@ def test_prefill_rejects_bad_rows_and_plans():
     bad = oa.PrefillPlan.from_buffer_copy(good)
     bad.hk = 0
     assert L.omni_attn_prefill_run(ctypes.byref(bad), f, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
-    bad = oa.PrefillPlan.from_buffer_copy(good)
-    bad.page = 12
-    assert L.omni_attn_prefill_run(ctypes.byref(bad), f, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
+    # Fields that disagree with each other: the grid, the item count and the
+    # tile shape come from the plan, so any edit is refused before a launch
+    # (too few workgroups would skip items silently).
+    for field, value in [("page", 0), ("workgroups", 0), ("workgroups", good.workgroups - 8),
+                         ("workgroups", good.workgroups + 8), ("tiles", good.tiles + 1), ("tile_rows", 128),
+                         ("hq", 8 * 16), ("hq", 8 * 3), ("work_bytes", good.work_bytes - 4)]:
+        bad = oa.PrefillPlan.from_buffer_copy(good)
+        setattr(bad, field, value)
+        assert L.omni_attn_prefill_run(ctypes.byref(bad), f, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL, field
     assert L.omni_attn_prefill_run(ctypes.byref(good), odd, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
 
 

@@ -69,20 +69,36 @@ def test_lastlen_encoding_is_identical():
     assert np.array_equal(host_bits(d.out), a)
 
 
-def test_gather_bit_exact(oracle):
-    c = W.paged_decode_case(6, 8, 4, 1, 700, seed=15, slack_pages=5)
+@pytest.mark.parametrize("page", [16, 1, 3, 12, 24, 48])
+def test_gather_bit_exact(oracle, page):
+    """The page-table gather is byte-equal to the oracle's, for power-of-two
+    pages and for the sizes only the division path serves."""
+    c = W.paged_decode_case(6, 8, 4, 1, 700, page=page, seed=15, slack_pages=5)
     d = DevPaged(c)
     lens = c.lens().astype(np.int32)
     ids = np.array([3, 0, 5, 1], np.int32)
     sel = lens[ids]
     out_indptr = np.concatenate([[0], np.cumsum(sel)]).astype(np.int32)
     out = torch.zeros(int(out_indptr[-1]), 2 * c.hk * 128, dtype=torch.bfloat16, device="cuda")
-    oa.gather_kv(d.kv, c.hk, d.indptr, d.pages, 16, dev_i32(ids), dev_i32(sel), dev_i32(out_indptr), out)
+    oa.gather_kv(d.kv, c.hk, d.indptr, d.pages, page, dev_i32(ids), dev_i32(sel), dev_i32(out_indptr), out)
     torch.cuda.synchronize()
     got = host_bits(out)
     for j, s in enumerate(ids):
-        want = oracle.gather_kv(c.kv, c.hk, c.indptr, c.pages, 16, int(s), int(sel[j]))
+        want = oracle.gather_kv(c.kv, c.hk, c.indptr, c.pages, page, int(s), int(sel[j]))
         assert np.array_equal(got[out_indptr[j]:out_indptr[j + 1]], want)
+
+
+@pytest.mark.parametrize("page", [12, 24])
+def test_page_permutation_is_bit_identical_any_page(page):
+    """Non-power-of-two pages: permuting the physical pages (and the table with
+    them) leaves the decode output bit-identical."""
+    c = W.paged_decode_case(6, 16, 8, 50, 900, page=page, seed=16, slack_pages=9)
+    a = DevPaged(c).decode(chunk=256)
+    perm = np.random.default_rng(2).permutation(c.num_pages).astype(np.int32)
+    kv2 = np.empty_like(c.kv)
+    kv2.reshape(c.num_pages, page, -1)[perm] = c.kv.reshape(c.num_pages, page, -1)
+    c.kv, c.pages = kv2, perm[c.pages].copy()
+    assert np.array_equal(DevPaged(c).decode(chunk=256), a)
 
 
 def test_page_permutation_is_bit_identical():
@@ -186,3 +202,24 @@ def test_long_contexts(oracle, chunk):
     far past the configs' 3000-key bound."""
     c = W.paged_decode_case(3, 8, 2, 20000, 65536, seed=15)  # 8q/2kv: a 1 KiB slot keeps the pool small
     assert_close(DevPaged(c).decode(chunk=chunk), oracle_out(oracle, c), what=f"long contexts chunk {chunk}")
+
+
+@pytest.mark.parametrize("splits", [3, 5, 6, 7])
+def test_every_split_written_once(oracle, splits):
+    """Split counts that are not powers of two (the rotated slot -> split map
+    has a period of 8 units there): the workspace starts as NaN, so a split
+    the kernel skipped or a partial left from an earlier call would show up
+    in the output. Rows of every length up to the plan's bound, MHA and GQA."""
+    for hq, hk in ((8, 8), (16, 8)):
+        max_len = 128 * splits
+        c = W.paged_decode_case(37, hq, hk, 1, max_len, seed=100 + splits, slack_pages=2)
+        d = DevPaged(c)
+        plan = oa.decode_plan(c.rows, hq, hk, 16, max_len, 128)
+        assert plan.splits == splits
+        ws = oa.workspace_for(plan)
+        ws.view(torch.float32).fill_(float("nan"))
+        oa.qwen3_attend(d.qkv, d.kv, d.pos, d.seq, 0, d.indptr, d.pages, 16, d.out, hq, hk, c.scale, plan, ws)
+        torch.cuda.synchronize()
+        assert_close(host_bits(d.out), oracle.paged_attend(c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, 16, hq,
+                                                           hk, c.scale, nthreads=16),
+                     what=f"{hq}/{hk} splits {splits}")

@@ -38,10 +38,12 @@ def test_fp8_parity(oracle, heads, lo, hi, ctx, chunk):
 
 
 @pytest.mark.parametrize("gh", [1, 2, 4, 8])
-@pytest.mark.parametrize("page", [1, 4, 16])
+@pytest.mark.parametrize("page", [1, 4, 16, 3, 12, 24])
 def test_fp8_heads_per_workgroup(oracle, gh, page):
     """Every heads-per-workgroup layout (1/2/4/8 heads, 8/4/2/1 keys per load),
-    over pages smaller and larger than a load's key group."""
+    over pages smaller and larger than a load's key group, powers of two
+    (shift and mask) and not (multiply-high division; 12 and 24 share one
+    page id per load group where the group divides them)."""
     c = W.fp8_ring_case(5, 8, 1, 700, 500, page=page, seed=gh * 31 + page, slack_pages=2)
     assert_close(run_fp8(c, 8, 128, group_heads=gh), oracle_fp8(oracle, c, 8), what=f"fp8 gh{gh} page{page}")
 

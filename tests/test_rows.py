@@ -29,6 +29,18 @@ def test_push_seq_matches_the_closed_form():
     assert np.array_equal(r.slot, slot)
 
 
+@pytest.mark.parametrize("page", [1, 3, 12, 24, 48])
+def test_any_page_size_follows_the_slot_rule(page):
+    """pages[t / page] * page + t % page for page sizes that are not powers of
+    two as well (the reference's slot rule divides)."""
+    r = oa.Rows(page=page, ring=0)
+    lease = np.array([9, 2, 14, 5, 0], np.int32)
+    count = 5 * page - 1
+    r.push(lease, 1, count, 0)
+    q = np.arange(1, 1 + count)
+    assert np.array_equal(r.slot, lease[q // page] * page + q % page)
+
+
 def test_ring_slots_wrap_at_the_context():
     r = oa.Rows(page=16, ring=40)
     lease = np.array([7, 3, 11], np.int32)  # 48 slots cover a 40-position ring
@@ -47,7 +59,7 @@ def test_lease_coverage_and_arguments_are_checked():
         r.push(np.array([1, -2], np.int32), 0, 3, 0)
     assert e.value.code == oa.ETABLE
     with pytest.raises(oa.OmniAttnError):
-        oa.Rows(page=12)
+        oa.Rows(page=0)
     assert r.counts() == (0, 0, 0)  # failed pushes leave nothing behind
     r.push(np.array([4], np.int32), 0, 16, 0)
     r.clear()

@@ -1,5 +1,5 @@
 """Seeded random sweeps of every attention kernel against the CPU oracle:
-shapes, GQA ratios, page sizes, lengths, splits and modes drawn per case
+shapes, GQA ratios, page sizes (powers of two and not), lengths, splits and modes drawn per case
 (ragged prefill rows also through the split-K decode kernel)
 from a generator seeded by the case number, so any failure names a case
 that reruns exactly. Sizes stay small enough for the oracle to finish in
@@ -15,6 +15,10 @@ from gpu_util import assert_close, dev_bits, dev_i32, host_bits
 pytestmark = pytest.mark.gpu
 
 CASES = range(24)
+# Page sizes drawn: powers of two (shift-and-mask kernels) and others (the
+# multiply-high division kernels; 12, 24 and 48 keep the scalar page-id paths
+# of the decode, FP8 and prefill loaders, 3 and 20 the per-lane ones).
+PAGES = [1, 2, 3, 4, 8, 12, 16, 20, 24, 32, 48, 64]
 
 
 def _paged_oracle(oracle, c):
@@ -30,7 +34,7 @@ def test_decode_sweep(oracle, case):
         hq = hk = int(rng.choice([4, 8, 32]))
     else:
         hq, hk = [(16, 8), (32, 8), (8, 8), (32, 32), (16, 4), (8, 2)][rng.integers(0, 6)]
-    page = int(rng.choice([1, 2, 4, 8, 16, 32, 64]))
+    page = int(rng.choice(PAGES))
     rows = int(rng.integers(1, 49))
     lo = int(rng.integers(1, 600))
     hi = lo + int(rng.integers(0, 1200))
@@ -54,7 +58,7 @@ def test_decode_sweep(oracle, case):
 def test_fp8_decode_sweep(oracle, case):
     rng = np.random.default_rng(2000 + case)
     heads = int(rng.choice([2, 4, 8, 16, 32]))
-    page = int(rng.choice([1, 2, 4, 8, 16, 32]))
+    page = int(rng.choice(PAGES))
     rows = int(rng.integers(1, 41))
     lo = int(rng.integers(1, 500))
     hi = lo + int(rng.integers(0, 1000))
@@ -80,7 +84,7 @@ def test_prefill_sweep(oracle, case):
     rng = np.random.default_rng(3000 + case)
     hk = int(rng.choice([1, 2, 4, 8]))
     hq = hk * int(rng.choice([1, 2, 4, 8]))
-    page = int(rng.choice([1, 2, 4, 8, 16, 32, 64]))
+    page = int(rng.choice(PAGES))
     nseq = int(rng.integers(1, 5))
     new_hi = int(rng.integers(1, 300))
     cached_hi = int(rng.integers(0, 300))

@@ -32,6 +32,15 @@ def test_prefill_parity(oracle, hq, hk):
     assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill {hq}/{hk}")
 
 
+@pytest.mark.parametrize("page", [3, 12, 24, 48, 80])
+def test_prefill_any_page(oracle, page):
+    """Pages that are not powers of two: 48 and 80 (multiples of a wave's 16
+    tile rows) take the one-page-id-per-wave loader with a multiply-high
+    division, 3, 12 and 24 the per-key loader."""
+    c = W.ragged_prefill_case(3, 32, 8, 1, 300, 0, 200, page=page, seed=page, slack_pages=3)
+    assert_close(run_prefill(c), oracle_paged(oracle, c), what=f"prefill page {page}")
+
+
 def test_prefill_single_rows_and_odd_lengths(oracle):
     c = W.ragged_prefill_case(6, 32, 8, 1, 3, 0, 70, seed=3)
     assert_close(run_prefill(c), oracle_paged(oracle, c), what="short")
@@ -179,6 +188,25 @@ def test_dit_tail_split_config5_matches_unsplit(oracle):
                                nthreads=16)
     assert_close(got[1, -128:], tail, what="config5 split tail vs oracle")
     del sub
+
+
+def test_dit_mha_config5_full_size(oracle):
+    """The hk = 32 (MHA) variant of config 5 at its full size: the CFG pair,
+    32 heads, 4352 queries and keys. On a 256-CU GPU its 1088 items run as
+    1024 whole and 64 split into 4 key chunks with a workspace (tiled_attn<1>
+    with the tail split, the kernel bench.py times), and as row halves without
+    one. Both agree on every row, and each batch half's first and last 128
+    query positions (whole and split tiles) meet the oracle."""
+    c = W.dense_case(32, 32, 4352, 4352, 0, batch=2, seed=5032)
+    got, ref = run_dense_ws(c), run_dense(c)
+    for b in range(2):
+        assert_close(got[b], ref[b], what=f"mha ws vs unsplit batch {b}")
+        for name, rows in (("first", slice(0, 128)), ("last", slice(4352 - 128, 4352))):
+            want = oracle.dense_attend(np.ascontiguousarray(c.q[b, rows]), np.ascontiguousarray(c.k[b]),
+                                       np.ascontiguousarray(c.v[b]), 128, 4352, c.q_stride, 32, 32, 0, c.scale_log2,
+                                       nthreads=16)
+            assert_close(got[b, rows], want, what=f"mha config5 batch {b} {name} 128 rows (workspace)")
+            assert_close(ref[b, rows], want, what=f"mha config5 batch {b} {name} 128 rows (no workspace)")
 
 
 @pytest.mark.parametrize("causal", [0, 1])

@@ -3,7 +3,8 @@ per-GPU scratch) against omni_qwen3_attend with a caller workspace, through
 the C ABI: two calls in a row on one GPU, the second with fewer rows and
 shorter rows (the scratch keeps the first call's partials), each compared
 bit for bit (the same kernels on the same inputs), and both with the oracle.
-Also the size limit: a plan above the scratch is rejected before launch."""
+Also the size limit: a plan above the scratch is rejected before launch, and
+the first call of a process made under HIP graph capture."""
 import ctypes
 
 import numpy as np
@@ -28,6 +29,32 @@ def _both(case, chunk):
                             plan)
     torch.cuda.synchronize()
     return host_bits(out), want
+
+
+# First in this file on purpose: in a process that has made no allocation-free
+# call yet, this one makes the library look up its static scratch while the
+# stream is being captured.
+def test_noalloc_first_call_inside_graph_capture():
+    """The entry point's advertised use: captured into a HIP graph (here its
+    first call in the process, so the per-device scratch lookup happens under
+    capture), replayed twice with eager work in between, each replay equal
+    bit for bit to omni_qwen3_attend with a caller workspace."""
+    c = W.paged_decode_case(24, 16, 8, 100, 1500, seed=73)
+    d = DevPaged(c)
+    plan = oa.decode_plan(c.rows, c.hq, c.hk, c.page, int(c.lens().max()), 256)
+    assert plan.splits > 1
+    want = d.decode(chunk=256)
+    out = torch.full((c.rows, c.hq * 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        oa.qwen3_attend_noalloc(d.qkv, d.kv, d.pos, d.seq, c.ragged, d.indptr, d.pages, c.page, out, c.hq, c.hk,
+                                c.scale, plan)
+    for rep in range(2):
+        out.fill_(float("nan"))
+        d.decode(chunk=256)  # eager work (the workspace call) between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host_bits(out), want), f"replay {rep} differs from the workspace call"
 
 
 def test_noalloc_matches_workspace_call_twice(oracle):
