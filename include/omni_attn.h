@@ -58,7 +58,8 @@ typedef struct omni_attn_decode_plan {
   int32_t max_len;  /* bound on keys any row sees; longer rows still run, slower */
   int32_t chunk;    /* keys per split (a multiple of 128) */
   int32_t splits;   /* ceil(max_len / chunk): workgroups per (row, kv head) */
-  int32_t group_heads; /* FP8 kernel: heads per workgroup, 1/2/4/8 dividing hk; 0 (what
+  int32_t group_heads; /* MHA kernels (hq == hk): heads per workgroup dividing hk, 1/2/4/8
+                          over FP8 slots, 1/2/4 over bf16 slots (paged rows); 0 (what
                           plan_init sets) picks from the shape */
   int64_t workspace_bytes; /* device scratch `*_run` needs (split partials) */
 } omni_attn_decode_plan;

@@ -290,6 +290,169 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   merge_waves<G>(a, n, kh, split, nsplit, len, sm_m, sm_l, sm_o);
 }
 
+// ---------------------------------------------------- MHA over bf16 slots
+//
+// lm_attend's semantics over bf16 slots (one q head per K/V head), with H
+// adjacent heads per workgroup so that every load instruction reads whole
+// contiguous runs of a slot: lane (r, hl, c) = (lane / 16H, lane / 16 % H,
+// lane % 16) owns the 16-byte chunk c of head kg H + hl of key row r, so one
+// load instruction moves R = 4 / H keys x H heads x 256 bytes (H = 4: one key's
+// 1 KB run of four heads' K rows, and of their V rows). A read probe of these
+// patterns over random 16-slot pages of 16 KB slots streams 7.09-7.13 TB/s for
+// four heads over 256 keys per workgroup against 6.77-6.83 TB/s for one head
+// over 1024 (the G = 1 layout of decode_split). Everything else is decode_split's
+// G = 1 path: two register tiles, base-2 online softmax with the scale in q,
+// per-lane V accumulation, waves merged in LDS and splits by decode_combine.
+// The grid is one-dimensional, split index fastest, then head group, then row,
+// so the H-head groups of one row run close together.
+
+// Combine the R = 4 / H key rows of a wave (lanes 16H apart), per lane.
+template <int H, bool MAX>
+__device__ __forceinline__ float across_key_rows16(float v) {
+  if constexpr (H == 1) v = MAX ? fmaxf(v, xor_lane(v, 16)) : v + xor_lane(v, 16);
+  if constexpr (H <= 2) v = MAX ? fmaxf(v, xor_lane(v, 32)) : v + xor_lane(v, 32);
+  return v;
+}
+
+template <int H, bool UP, bool DIV>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_mh(DecodeArgs a, int rows) {
+  constexpr int R = 4 / H;       // keys per load instruction
+  constexpr int NI = 8;          // load instructions per wave and tile
+  constexpr int kKeys = R * NI;  // keys per wave and tile
+  const int groups = a.hk / H;
+  const int slot = (int)blockIdx.x % a.splits, rest = (int)blockIdx.x / a.splits;
+  const int kg = rest % groups, n = rest / groups;
+  if (n >= rows) return;
+  const int split = rotated_split(slot, kg + groups * n, a.splits);
+  const int s = a.ragged ? a.seq[n] : n;
+  const int len = decode_len(a, n, s);
+  const int split_len = decode_split_len(a, len);
+  const int nsplit = decode_nsplit(len, split_len);
+  if (split >= nsplit) return;
+  const int t0 = split * split_len;
+  const int t1 = min(len, t0 + split_len);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane / (16 * H), hl = (lane >> 4) % H, c = lane & 15;
+  const int kh = kg * H + hl;
+
+  float q[8];
+  widen8(ldg16(a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * kHead + c * 8), q);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] *= a.scale_log2;
+
+  const int32_t* pg = a.pages + a.indptr[s];
+  const int64_t per_slot = 2LL * a.hk * kHead;
+  const bf16_t* kb = a.kv + (int64_t)kh * kHead + c * 8;
+  const bf16_t* vb = a.kv + (int64_t)(a.hk + kh) * kHead + c * 8;
+
+  float m = -INFINITY, l = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+
+  // Key tb + R i + r, clamped to the split (a clamped key has p = 0 and reads
+  // a valid slot). UP: the R keys of one instruction share a page (page a
+  // multiple of R), so its id is a scalar load.
+  auto page_of = [&](int tb, int i) -> int {
+    if constexpr (UP)
+      return pg[key_page<DIV>(a.pd, __builtin_amdgcn_readfirstlane(min(tb + R * i, t1 - 1)))];
+    else
+      return pg[key_page<DIV>(a.pd, min(tb + R * i + r, t1 - 1))];
+  };
+  struct KVTile {
+    uint4 kr[NI], vr[NI];
+  };
+  auto load_tile = [&](KVTile& x, int tb, const int* pid) __attribute__((always_inline)) {
+    int64_t off[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) off[i] = key_slot<DIV>(a.pd, pid[i], min(tb + R * i + r, t1 - 1)) * per_slot;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) x.kr[i] = ldg16_stream(kb + off[i]);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) x.vr[i] = ldg16_stream(vb + off[i]);
+  };
+  auto compute_tile = [&](const KVTile& x, int tb) __attribute__((always_inline)) {
+    float sc[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float kf[8];
+      widen8(x.kr[i], kf);
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(q[e], kf[e], d);
+      d = row16_sum(d);
+      sc[i] = tb + R * i + r < t1 ? d : -INFINITY;
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < NI; ++i) mx = fmaxf(mx, sc[i]);
+    mx = across_key_rows16<H, true>(mx);
+    const float mn = fmaxf(m, mx);
+    const float corr = fast_exp2(m - mn);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      sc[i] = fast_exp2(sc[i] - mn);
+      ps += sc[i];
+    }
+    l = fmaf(l, corr, ps);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= corr;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float vf[8];
+      widen8(x.vr[i], vf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(sc[i], vf[e], acc[e]);
+    }
+  };
+  constexpr int kStride = kDecodeWaves * kKeys;
+  const int tb0 = t0 + wave * kKeys;
+  if (tb0 < t1) {
+    int pid[NI];
+    KVTile ta, tn;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0, i);
+    load_tile(ta, tb0, pid);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0 + kStride, i);
+    for (int tb = tb0;; tb += 2 * kStride) {
+      load_tile(tn, tb + kStride, pid);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + 2 * kStride, i);
+      __builtin_amdgcn_sched_barrier(0);  // keep the next tile's loads ahead of this tile's math
+      compute_tile(ta, tb);
+      if (tb + kStride >= t1) break;
+      load_tile(ta, tb + 2 * kStride, pid);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + 3 * kStride, i);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_tile(tn, tb + kStride);
+      if (tb + 2 * kStride >= t1) break;
+    }
+  }
+
+  // The key rows of the wave hold disjoint keys under one shared max.
+  l = across_key_rows16<H, false>(l);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = across_key_rows16<H, false>(acc[e]);
+  __shared__ float sm_m[kDecodeWaves][H], sm_l[kDecodeWaves][H];
+  __shared__ float sm_o[kDecodeWaves][H][kHead];
+  if (r == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm_o[wave][hl][c * 8 + e] = acc[e];
+    if (c == 0) {
+      sm_m[wave][hl] = m;
+      sm_l[wave][hl] = l;
+    }
+  }
+  __syncthreads();
+  // Heads kg H .. kg H + H - 1 are q heads kh G + g of merge_waves with G = H.
+  merge_waves<H>(a, n, kg, split, nsplit, len, sm_m, sm_l, sm_o);
+}
+
 // ------------------------------------------------------------------ FP8 slots
 //
 // lm_attend's real cache (crates/omni-personaplex/kernels/lm.cu:196-290): a
@@ -594,6 +757,40 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
    : div                           ? K<G, kSlotsLane, true><<<grid, kDecodeThreads, 0, stream>>>(a)    \
    : slots == kSlotsUniform        ? K<G, kSlotsUniform, false><<<grid, kDecodeThreads, 0, stream>>>(a) \
                                    : K<G, kSlotsLane, false><<<grid, kDecodeThreads, 0, stream>>>(a))
+  // MHA over bf16 slots: H heads per workgroup (the plan's group_heads, or 2
+  // when that still leaves >= 2048 workgroups). Measured on the 128-session
+  // tick: H = 2 505-508 us against 512-515 for H = 1, H = 4 526-540.
+  int mh = 0;
+  if (a.hq == a.hk && slots != kSlotsDense)
+    mh = a.group_heads > 0 ? a.group_heads
+                           : (a.hk % 2 == 0 && (int64_t)rows * (a.hk / 2) * a.splits >= 2048 ? 2 : 1);
+  if (mh > 1) {
+    const int H = mh;
+    const dim3 g1((unsigned)(rows * (a.hk / H) * a.splits));
+#define OMNI_MH(HH)                                                                                      \
+  {                                                                                                      \
+    constexpr int kR = 4 / HH;                                                                           \
+    const bool up = a.pd.page % kR == 0;                                                                 \
+    if (div)                                                                                             \
+      up ? decode_split_mh<HH, true, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows)                   \
+         : decode_split_mh<HH, false, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows);                 \
+    else                                                                                                 \
+      up ? decode_split_mh<HH, true, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows)                  \
+         : decode_split_mh<HH, false, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows);                \
+  }
+    switch (H) {
+      case 4: OMNI_MH(4) break;
+      case 2: OMNI_MH(2) break;
+      default: return -2;
+    }
+#undef OMNI_MH
+    if (check_launch() != 0) return -3;
+    if (a.splits > 1) {
+      decode_combine<<<dim3(a.hq, rows), 64, 0, stream>>>(a);
+      if (check_launch() != 0) return -3;
+    }
+    return 0;
+  }
   switch (a.hq / a.hk) {
     case 1: OMNI_DECODE(decode_split, 1); break;
     case 2: OMNI_DECODE(decode_split, 2); break;

@@ -70,6 +70,18 @@ def test_run_without_workspace_fails_before_launch():
     assert rc == oa.EINVAL
 
 
+@pytest.mark.parametrize("gh,hq,hk", [(3, 8, 8), (8, 8, 8), (-1, 8, 8), (2, 16, 8), (4, 4, 2)])
+def test_bf16_group_heads_validated_before_launch(gh, hq, hk):
+    """bf16 slots take 1, 2 or 4 heads per workgroup dividing hk, MHA only."""
+    p = oa.decode_plan(4, hq, hk, 16, 1000, chunk=128)
+    p.group_heads = gh
+    fake = ctypes.c_void_p(16)
+    rc = oa.load().omni_qwen3_attend(fake, fake, fake, None, 0, fake, fake, 16, fake, hq, hk, 0.1, ctypes.byref(p),
+                                     fake, None)
+    assert rc == oa.EINVAL
+    assert "group_heads" in oa.load().omni_attn_last_error().decode()
+
+
 @pytest.mark.parametrize("gh", [3, 16, -2, 6])
 def test_fp8_group_heads_validated_before_launch(gh):
     p = oa.decode_plan(4, 8, 8, 16, 1000, chunk=128)

@@ -223,3 +223,46 @@ def test_every_split_written_once(oracle, splits):
         assert_close(host_bits(d.out), oracle.paged_attend(c.qkv, c.kv, c.pos, c.seq, 0, c.indptr, c.pages, 16, hq,
                                                            hk, c.scale, nthreads=16),
                      what=f"{hq}/{hk} splits {splits}")
+
+
+@pytest.mark.parametrize("gh", [0, 1, 2, 4])
+@pytest.mark.parametrize("page", [1, 3, 12, 16])
+def test_mha_heads_per_workgroup(oracle, gh, page):
+    """MHA over bf16 slots with one head per workgroup (decode_split<1>) or 2
+    and 4 adjacent heads (decode_split_mh<H>, whose load instructions read
+    4 / H keys x H heads), with and without the ring cap, over pages smaller
+    and larger than a load's key group, powers of two and not."""
+    for lm in (True, False):
+        c = W.paged_decode_case(7, 8, 8, 1, 900, page=page, seed=gh * 31 + page, context=600 if lm else 0,
+                                slack_pages=2)
+        d = DevPaged(c)
+        plan = oa.decode_plan(c.rows, 8, 8, page, int(c.lens().max()), 128)
+        plan.group_heads = gh
+        ws = oa.workspace_for(plan)
+        args = (d.qkv, d.kv, d.pos, d.seq, 0, d.indptr, d.pages, page, d.out)
+        if lm:
+            oa.lm_attend(*args, 8, c.scale, c.context, plan, ws)
+        else:
+            oa.qwen3_attend(*args, 8, 8, c.scale, plan, ws)
+        torch.cuda.synchronize()
+        assert_close(host_bits(d.out), oracle_out(oracle, c), what=f"mha gh {gh} page {page} lm {lm}")
+
+
+def test_mha_head_groups_agree_with_one_head_kernel(oracle):
+    """The headline's shape class (MHA, 32 heads, 96 rows of up to 3000 keys,
+    ring 3000, 1024-key splits): the 2-head kernel the plan picks there and the
+    one-head kernel give the same rows to the tolerance, and both meet the
+    oracle."""
+    c = W.paged_decode_case(96, 32, 32, 100, 3000, seed=33, context=3000)
+    d = DevPaged(c)
+    outs = []
+    for gh in (0, 1):
+        plan = oa.decode_plan(c.rows, 32, 32, 16, 3000, 1024)
+        plan.group_heads = gh
+        d.out.zero_()
+        oa.lm_attend(d.qkv, d.kv, d.pos, d.seq, 0, d.indptr, d.pages, 16, d.out, 32, c.scale, 3000, plan,
+                     oa.workspace_for(plan))
+        torch.cuda.synchronize()
+        outs.append(host_bits(d.out))
+    assert_close(outs[0], outs[1], what="2-head vs 1-head kernel")
+    assert_close(outs[0], oracle_out(oracle, c, threads=16), what="2-head kernel vs oracle")
