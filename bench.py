@@ -59,7 +59,7 @@ class DecodeBench:
     larger than the 256 MB last-level cache) cycled over the layers, each
     layer with its own random page table."""
 
-    def __init__(self, cfg, pools, seed=0, chunk=0, fp8=False):
+    def __init__(self, cfg, pools, seed=0, chunk=0, fp8=False, group_heads=0):
         import numpy as np
         import torch
 
@@ -98,6 +98,7 @@ class DecodeBench:
                                  out=torch.empty(case.rows, case.hq * 128, dtype=torch.bfloat16, device="cuda")))
         c0 = self.cases[0]
         self.plan = oa.decode_plan(c0.rows, c0.hq, c0.hk, c0.page, c["len_hi"] if not self.lm else c["context"], chunk)
+        self.plan.group_heads = group_heads
         self.ws = oa.workspace_for(self.plan)
         self.bytes_per_layer = [W.fp8_kv_bytes(cs) if fp8 else cs.kv_bytes() for cs in self.cases]
         self.oa = oa
@@ -678,7 +679,7 @@ def headline_bench(args, stream):
 
     cfg = 3
     log(f"[bench] decode config {cfg}: building workload")
-    b = DecodeBench(cfg, args.pools, chunk=args.chunk)
+    b = DecodeBench(cfg, args.pools, chunk=args.chunk, group_heads=args.group_heads)
     log(f"[bench] decode config {cfg}: plan chunk={b.plan.chunk} splits={b.plan.splits}; timing")
     ms, launch_ms = time_steps(lambda s, e: b.step(s, e), args.steps, args.warmup, stream, per_launch=b.layers)
     total_bytes = sum(b.bytes_per_layer)
@@ -702,6 +703,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--pools", type=int, default=4)
     ap.add_argument("--chunk", type=int, default=0)
+    ap.add_argument("--group-heads", type=int, default=0,
+                    help="K/V heads per decode workgroup (the plan's group_heads; 0 = the plan's pick)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the HIP-graph replays (profiling runs: the trace then ends on the timed calls)")
@@ -766,7 +769,7 @@ def main():
             extra[key]["frac_of_measured_random_peak"] = round(extra[key]["frac"] * BF16_PEAK_TFLOPS / rnd, 4)
     if args.only in (0, 2):
         log("[bench] config 2 decode")
-        b2 = DecodeBench(2, args.pools, chunk=args.chunk)
+        b2 = DecodeBench(2, args.pools, chunk=args.chunk, group_heads=args.group_heads)
         ms2, l2 = time_steps(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream, per_launch=b2.layers)
         g2 = float("nan") if args.no_graph else graph_step_ms(lambda s, e: b2.step(s, e), args.steps, args.warmup,
                                                                stream)

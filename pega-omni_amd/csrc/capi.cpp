@@ -84,10 +84,11 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   const int gh = plan->group_heads;
   if (fp8 && gh != 0 && (gh < 0 || (gh & (gh - 1)) != 0 || gh > 8 || hk % gh != 0))
     return fail(OMNI_ATTN_EINVAL, "decode: plan group_heads=%d is not 1, 2, 4 or 8 dividing heads=%d", gh, hk);
-  if (!fp8 && gh != 0 && (hq != hk || len_mode == 2 || (gh != 1 && gh != 2 && gh != 4) || hk % gh != 0))
+  if (!fp8 && gh != 0 &&
+      (len_mode == 2 || (gh != 1 && gh != 2 && gh != 4) || hk % gh != 0 || (hq / hk == 4 && gh == 4)))
     return fail(OMNI_ATTN_EINVAL,
-                "decode: plan group_heads=%d: bf16 slots take 1, 2 or 4 dividing heads=%d, and only for MHA paged rows",
-                gh, hk);
+                "decode: plan group_heads=%d: paged bf16 slots take 1, 2 or 4 dividing hk=%d (1 or 2 when hq = 4 hk)", gh,
+                hk);
   omni::DecodeArgs a{};
   a.qkv = static_cast<const omni::bf16_t*>(qkv);
   a.q_stride = (int64_t)(hq + 2 * hk) * OMNI_ATTN_HEAD_DIM;

@@ -314,7 +314,7 @@ __device__ __forceinline__ float across_key_rows16(float v) {
   return v;
 }
 
-template <int H, bool UP, bool DIV>
+template <int G, int H, bool UP, bool DIV>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_mh(DecodeArgs a, int rows) {
   constexpr int R = 4 / H;       // keys per load instruction
   constexpr int NI = 8;          // load instructions per wave and tile
@@ -337,19 +337,29 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_mh(DecodeArgs a, 
   const int r = lane / (16 * H), hl = (lane >> 4) % H, c = lane & 15;
   const int kh = kg * H + hl;
 
-  float q[8];
-  widen8(ldg16(a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * kHead + c * 8), q);
+  // The G query heads kh G .. kh G + G - 1 that share K/V head kh.
+  float q[G][8];
+  const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * G * kHead + c * 8;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) q[e] *= a.scale_log2;
+  for (int g = 0; g < G; ++g) {
+    widen8(ldg16(qp + g * kHead), q[g]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[g][e] *= a.scale_log2;
+  }
 
   const int32_t* pg = a.pages + a.indptr[s];
   const int64_t per_slot = 2LL * a.hk * kHead;
   const bf16_t* kb = a.kv + (int64_t)kh * kHead + c * 8;
   const bf16_t* vb = a.kv + (int64_t)(a.hk + kh) * kHead + c * 8;
 
-  float m = -INFINITY, l = 0.f, acc[8];
+  float m[G], l[G], acc[G][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
 
   // Key tb + R i + r, clamped to the split (a clamped key has p = 0 and reads
   // a valid slot). UP: the R keys of one instruction share a page (page a
@@ -373,44 +383,67 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_mh(DecodeArgs a, 
     for (int i = 0; i < NI; ++i) x.vr[i] = ldg16_stream(vb + off[i]);
   };
   auto compute_tile = [&](const KVTile& x, int tb) __attribute__((always_inline)) {
-    float sc[NI];
+    float sc[G][NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       float kf[8];
       widen8(x.kr[i], kf);
-      float d = 0.f;
+      const bool valid = tb + R * i + r < t1;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(q[e], kf[e], d);
-      d = row16_sum(d);
-      sc[i] = tb + R * i + r < t1 ? d : -INFINITY;
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(q[g][e], kf[e], d);
+        d = row16_sum(d);
+        sc[g][i] = valid ? d : -INFINITY;
+      }
     }
-    float mx = sc[0];
 #pragma unroll
-    for (int i = 1; i < NI; ++i) mx = fmaxf(mx, sc[i]);
-    mx = across_key_rows16<H, true>(mx);
-    const float mn = fmaxf(m, mx);
-    const float corr = fast_exp2(m - mn);
-    m = mn;
-    float ps = 0.f;
+    for (int g = 0; g < G; ++g) {
+      float mx = sc[g][0];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      sc[i] = fast_exp2(sc[i] - mn);
-      ps += sc[i];
+      for (int i = 1; i < NI; ++i) mx = fmaxf(mx, sc[g][i]);
+      mx = across_key_rows16<H, true>(mx);
+      const float mn = fmaxf(m[g], mx);
+      const float corr = fast_exp2(m[g] - mn);
+      m[g] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        sc[g][i] = fast_exp2(sc[g][i] - mn);
+        ps += sc[g][i];
+      }
+      l[g] = fmaf(l[g], corr, ps);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= corr;
     }
-    l = fmaf(l, corr, ps);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= corr;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       float vf[8];
       widen8(x.vr[i], vf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(sc[i], vf[e], acc[e]);
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(sc[g][i], vf[e], acc[g][e]);
     }
   };
   constexpr int kStride = kDecodeWaves * kKeys;
   const int tb0 = t0 + wave * kKeys;
-  if (tb0 < t1) {
+  if (G > 1 && tb0 < t1) {
+    // One register tile at a time (as decode_split does for G > 1).
+    int pid[NI];
+    KVTile ta;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0, i);
+    for (int tb = tb0; tb < t1; tb += kStride) {
+      load_tile(ta, tb, pid);
+      if (tb + kStride < t1) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + kStride, i);
+      }
+      compute_tile(ta, tb);
+    }
+  } else if (tb0 < t1) {
     int pid[NI];
     KVTile ta, tn;
 #pragma unroll
@@ -435,22 +468,29 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_mh(DecodeArgs a, 
   }
 
   // The key rows of the wave hold disjoint keys under one shared max.
-  l = across_key_rows16<H, false>(l);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = across_key_rows16<H, false>(acc[e]);
-  __shared__ float sm_m[kDecodeWaves][H], sm_l[kDecodeWaves][H];
-  __shared__ float sm_o[kDecodeWaves][H][kHead];
+  for (int g = 0; g < G; ++g) {
+    l[g] = across_key_rows16<H, false>(l[g]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = across_key_rows16<H, false>(acc[g][e]);
+  }
+  __shared__ float sm_m[kDecodeWaves][H * G], sm_l[kDecodeWaves][H * G];
+  __shared__ float sm_o[kDecodeWaves][H * G][kHead];
   if (r == 0) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm_o[wave][hl][c * 8 + e] = acc[e];
-    if (c == 0) {
-      sm_m[wave][hl] = m;
-      sm_l[wave][hl] = l;
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm_o[wave][hl * G + g][c * 8 + e] = acc[g][e];
+      if (c == 0) {
+        sm_m[wave][hl * G + g] = m[g];
+        sm_l[wave][hl * G + g] = l[g];
+      }
     }
   }
   __syncthreads();
-  // Heads kg H .. kg H + H - 1 are q heads kh G + g of merge_waves with G = H.
-  merge_waves<H>(a, n, kg, split, nsplit, len, sm_m, sm_l, sm_o);
+  // K/V heads kg H .. kg H + H - 1 serve q heads kg H G .. kg H G + H G - 1:
+  // merge_waves with G' = H G and kv head index kg.
+  merge_waves<H * G>(a, n, kg, split, nsplit, len, sm_m, sm_l, sm_o);
 }
 
 // ------------------------------------------------------------------ FP8 slots
@@ -757,30 +797,34 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
    : div                           ? K<G, kSlotsLane, true><<<grid, kDecodeThreads, 0, stream>>>(a)    \
    : slots == kSlotsUniform        ? K<G, kSlotsUniform, false><<<grid, kDecodeThreads, 0, stream>>>(a) \
                                    : K<G, kSlotsLane, false><<<grid, kDecodeThreads, 0, stream>>>(a))
-  // MHA over bf16 slots: H heads per workgroup (the plan's group_heads, or 2
-  // when that still leaves >= 2048 workgroups). Measured on the 128-session
-  // tick: H = 2 505-508 us against 512-515 for H = 1, H = 4 526-540.
+  // Paged bf16 slots: H adjacent K/V heads per workgroup (the plan's
+  // group_heads; 0 picks 2 for MHA when that still leaves >= 2048 workgroups,
+  // else 1). Measured on the 128-session MHA tick: H = 2 505-508 us against
+  // 512-515 for H = 1, H = 4 526-540.
   int mh = 0;
-  if (a.hq == a.hk && slots != kSlotsDense)
+  if (slots != kSlotsDense)
     mh = a.group_heads > 0 ? a.group_heads
-                           : (a.hk % 2 == 0 && (int64_t)rows * (a.hk / 2) * a.splits >= 2048 ? 2 : 1);
+                           : (a.hq == a.hk && a.hk % 2 == 0 && (int64_t)rows * (a.hk / 2) * a.splits >= 2048 ? 2 : 1);
   if (mh > 1) {
     const int H = mh;
     const dim3 g1((unsigned)(rows * (a.hk / H) * a.splits));
-#define OMNI_MH(HH)                                                                                      \
+#define OMNI_MH(GG, HH)                                                                                  \
   {                                                                                                      \
     constexpr int kR = 4 / HH;                                                                           \
     const bool up = a.pd.page % kR == 0;                                                                 \
     if (div)                                                                                             \
-      up ? decode_split_mh<HH, true, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows)                   \
-         : decode_split_mh<HH, false, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows);                 \
+      up ? decode_split_mh<GG, HH, true, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows)               \
+         : decode_split_mh<GG, HH, false, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows);             \
     else                                                                                                 \
-      up ? decode_split_mh<HH, true, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows)                  \
-         : decode_split_mh<HH, false, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows);                \
+      up ? decode_split_mh<GG, HH, true, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows)              \
+         : decode_split_mh<GG, HH, false, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows);            \
   }
-    switch (H) {
-      case 4: OMNI_MH(4) break;
-      case 2: OMNI_MH(2) break;
+    switch (a.hq / a.hk * 8 + H) {
+      case 8 + 4: OMNI_MH(1, 4) break;
+      case 8 + 2: OMNI_MH(1, 2) break;
+      case 16 + 4: OMNI_MH(2, 4) break;
+      case 16 + 2: OMNI_MH(2, 2) break;
+      case 32 + 2: OMNI_MH(4, 2) break;
       default: return -2;
     }
 #undef OMNI_MH

@@ -70,9 +70,10 @@ def test_run_without_workspace_fails_before_launch():
     assert rc == oa.EINVAL
 
 
-@pytest.mark.parametrize("gh,hq,hk", [(3, 8, 8), (8, 8, 8), (-1, 8, 8), (2, 16, 8), (4, 4, 2)])
+@pytest.mark.parametrize("gh,hq,hk", [(3, 8, 8), (8, 8, 8), (-1, 8, 8), (4, 16, 4), (2, 4, 1), (4, 8, 2)])
 def test_bf16_group_heads_validated_before_launch(gh, hq, hk):
-    """bf16 slots take 1, 2 or 4 heads per workgroup dividing hk, MHA only."""
+    """bf16 slots take 1, 2 or 4 K/V heads per workgroup dividing hk (1 or 2
+    when four q heads share a K/V head)."""
     p = oa.decode_plan(4, hq, hk, 16, 1000, chunk=128)
     p.group_heads = gh
     fake = ctypes.c_void_p(16)

@@ -266,3 +266,18 @@ def test_mha_head_groups_agree_with_one_head_kernel(oracle):
         outs.append(host_bits(d.out))
     assert_close(outs[0], outs[1], what="2-head vs 1-head kernel")
     assert_close(outs[0], oracle_out(oracle, c, threads=16), what="2-head kernel vs oracle")
+
+
+@pytest.mark.parametrize("hq,hk,gh", [(16, 8, 2), (16, 8, 4), (32, 8, 2), (8, 4, 2)])
+@pytest.mark.parametrize("page", [16, 12])
+def test_gqa_head_groups(oracle, hq, hk, gh, page):
+    """GQA rows through the head-group kernel a plan's group_heads selects
+    (two or four K/V heads per workgroup, each with its G query heads)."""
+    c = W.paged_decode_case(9, hq, hk, 1, 1300, page=page, seed=hq + hk + gh + page, slack_pages=2)
+    d = DevPaged(c)
+    plan = oa.decode_plan(c.rows, hq, hk, page, int(c.lens().max()), 256)
+    plan.group_heads = gh
+    oa.qwen3_attend(d.qkv, d.kv, d.pos, d.seq, 0, d.indptr, d.pages, page, d.out, hq, hk, c.scale, plan,
+                    oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    assert_close(host_bits(d.out), oracle_out(oracle, c), what=f"gqa {hq}/{hk} gh {gh} page {page}")
