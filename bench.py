@@ -859,7 +859,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": DECODE_CFG3_TRAFFIC_BYTES if cfg == 3 else None,
-            "kernel": "decode_split<1, 1> + decode_combine (one lm_attend call)",
+            "kernel": "decode_split_mh<1, 2, true, false> + decode_combine (one lm_attend call)",
             "bytes_per_launch": per_launch_bytes,
             "launch_us": round(launch_ms * 1e3, 2),
         },
