@@ -28,7 +28,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE + WRITE_SIZE runs scaled by a 1 GiB copy's counts (the summary
 # and commands are in profiles/decode_config3_traffic.md). Re-measure when
 # the decode kernel changes.
-DECODE_CFG3_TRAFFIC_BYTES = 3.271e+09
+DECODE_CFG3_TRAFFIC_BYTES = 3.272e+09
 BF16_PEAK_TFLOPS = 2500.0
 
 
