@@ -56,11 +56,12 @@ class DevPaged:
         self.pages = dev_i32(case.pages)
         self.out = torch.zeros(case.rows, case.hq * 128, dtype=torch.bfloat16, device="cuda")
 
-    def decode(self, chunk=0, max_len=None, lm=False):
+    def decode(self, chunk=0, max_len=None, lm=False, group_heads=0):
         c = self.c
         if max_len is None:
             max_len = int(c.lens().max())
         plan = oa.decode_plan(c.rows, c.hq, c.hk, c.page, max_len, chunk)
+        plan.group_heads = group_heads
         ws = oa.workspace_for(plan)
         self.out.zero_()
         if lm:

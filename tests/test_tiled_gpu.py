@@ -68,14 +68,17 @@ def test_prefill_config4_own_draw(oracle):
     """Config 4's own seeded draw (B = 8, seed 4000: 25,499 rows, up to 4,563
     keys), the workload bench.py times, so its work-list order (longest tiles
     first, XCD ranges, the 8 sequences' items) is the one checked: the oracle
-    on the first and last 64 rows of every sequence plus 256 seeded random
-    rows, and the split-K decode kernel on every row."""
+    on the first and last 64 rows of every sequence, every 8th row (so every
+    64-position tile, each with all 8 kv heads' items, meets it at 8 rows)
+    plus 256 seeded random rows, about 4,400 rows in all; and the split-K
+    decode kernel (the reference's f32 P) on every row."""
     c = W.config_case(4)
     assert c.rows == 25499 and len(c.extra["new"]) == 8
     got = run_prefill(c)
     starts = np.concatenate([[0], np.cumsum(c.extra["new"])])
     idx = [np.arange(a, min(a + 64, b)) for a, b in zip(starts[:-1], starts[1:])]
     idx += [np.arange(max(b - 64, a), b) for a, b in zip(starts[:-1], starts[1:])]
+    idx.append(np.arange(0, c.rows, 8))
     idx.append(np.random.default_rng(4001).choice(c.rows, 256, replace=False))
     idx = np.unique(np.concatenate(idx))
     want = oracle.paged_attend(np.ascontiguousarray(c.qkv[idx]), c.kv, c.pos[idx].copy(), c.seq[idx].copy(), 1,
