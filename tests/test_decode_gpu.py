@@ -6,7 +6,7 @@ import torch
 
 import omni_attn as oa
 import workloads as W
-from gpu_util import DevPaged, assert_close, dev_i32, host_bits
+from gpu_util import DevPaged, assert_close, dev_bits, dev_i32, host_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -281,3 +281,31 @@ def test_gqa_head_groups(oracle, hq, hk, gh, page):
                     oa.workspace_for(plan))
     torch.cuda.synchronize()
     assert_close(host_bits(d.out), oracle_out(oracle, c), what=f"gqa {hq}/{hk} gh {gh} page {page}")
+
+
+@pytest.mark.parametrize("gh", [2, 4])
+def test_head_groups_ragged_and_last_page_lengths(oracle, gh):
+    """The head-group kernel on ragged prefill rows (qwen3_attend, ragged = 1)
+    and with per-sequence last-page lengths (decode_run_lastlen) in place of
+    positions."""
+    p = W.ragged_prefill_case(3, 8, 8, 1, 200, 0, 300, seed=50 + gh, slack_pages=2)
+    plan = oa.decode_plan(p.rows, 8, 8, 16, int(p.pos.max()) + 1, 128)
+    plan.group_heads = gh
+    out = torch.zeros(p.rows, 8 * 128, dtype=torch.bfloat16, device="cuda")
+    oa.qwen3_attend(dev_bits(p.qkv), dev_bits(p.kv), dev_i32(p.pos), dev_i32(p.seq), 1, dev_i32(p.indptr),
+                    dev_i32(p.pages), 16, out, 8, 8, p.scale, plan, oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    assert_close(host_bits(out), oracle_out(oracle, p, threads=16), what=f"ragged rows gh {gh}")
+
+    c = W.paged_decode_case(8, 8, 8, 1, 500, seed=60 + gh)
+    d = DevPaged(c)
+    want = d.decode(chunk=128, group_heads=gh)
+    last = ((c.pos % 16) + 1).astype(np.int32)
+    plan = oa.decode_plan(c.rows, 8, 8, 16, int(c.lens().max()), 128)
+    plan.group_heads = gh
+    d.out.zero_()
+    oa.decode_lastlen(d.qkv, d.kv, dev_i32(last), d.seq, 0, d.indptr, d.pages, 16, d.out, 8, 8, c.scale, plan,
+                      oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(d.out), want)
+    assert_close(want, oracle_out(oracle, c), what=f"gh {gh} vs oracle")
