@@ -117,7 +117,9 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.dense_base = dense_base;
   a.dense_span = dense_span;
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
-  if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d not in {1,2,4}", hq / hk);
+  if (rc == -2)
+    return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d and group_heads=%d not served, or the grid passes 2^31 "
+                "workgroups", hq / hk, plan->group_heads);
   if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "decode: launch failed: %s", hipGetErrorString(omni::g_launch_status));
   return ok();
 }

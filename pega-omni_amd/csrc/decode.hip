@@ -777,6 +777,8 @@ static void launch_fp8_h(const DecodeArgs& a, int rows, hipStream_t stream) {
 
 static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) {
   if (a.hq != a.hk) return -2;
+  // The one-dimensional grid (at most hk (rows splits + 7) workgroups) must fit an int.
+  if ((int64_t)a.hk * ((int64_t)rows * a.splits + 7) > INT32_MAX) return -2;
   switch (fp8_heads_per_group(a, rows)) {
     case 8: launch_fp8_h<8>(a, rows, stream); break;
     case 4: launch_fp8_h<4>(a, rows, stream); break;
@@ -807,10 +809,15 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   // group_heads; 0 picks 2 for MHA when that still leaves >= 2048 workgroups,
   // else 1). Measured on the 128-session MHA tick: H = 2 505-508 us against
   // 512-515 for H = 1, H = 4 526-540.
+  // The head-group kernel's one-dimensional grid (rows x hk / H x splits
+  // workgroups) must fit an int; the plan's pick falls back to one head per
+  // workgroup (a three-dimensional grid) when it would not.
+  const int64_t mh_units = (int64_t)rows * a.hk * a.splits;
   int mh = 0;
   if (slots != kSlotsDense)
     mh = a.group_heads > 0 ? a.group_heads
-                           : (a.hq == a.hk && a.hk % 2 == 0 && (int64_t)rows * (a.hk / 2) * a.splits >= 2048 ? 2 : 1);
+                           : (a.hq == a.hk && a.hk % 2 == 0 && mh_units / 2 >= 2048 && mh_units / 2 <= INT32_MAX ? 2 : 1);
+  if (mh > 1 && mh_units / mh > INT32_MAX) return -2;
   if (mh > 1) {
     const int H = mh;
     const dim3 g1((unsigned)(rows * (a.hk / H) * a.splits));
