@@ -701,8 +701,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
 // thread per dim, 0.2-0.4% faster on every decode workload). A thread's
 // loads (the row's split lse values and its dim of every split's partial) are
 // all issued before any is used, so the merge costs one memory round trip
-// rather than one per split (up to kCombineBatch splits per round trip).
-constexpr int kCombineBatch = 8;
+// rather than one per split (up to kCombineBatch splits per round trip; 12
+// covers the ten splits of the Qwen3-TTS bucket's 256-key plan in one: config 2
+// 63.2 against 63.6-63.7 us per call with 8).
+constexpr int kCombineBatch = 12;
 
 __global__ __launch_bounds__(64) void decode_combine(DecodeArgs a) {
   const int h = blockIdx.x, n = blockIdx.y, d = threadIdx.x;  // dims d and d + 64
