@@ -175,3 +175,46 @@ def test_dit_step_graph_replays():
         assert torch.equal(got_out.view(torch.int16), out.view(torch.int16)), f"replay {rep}: attention output"
         assert torch.equal(got_k.view(torch.int16), kc.view(torch.int16)), f"replay {rep}: K cache"
         assert torch.equal(got_q.view(torch.int16), qkv.view(torch.int16)), f"replay {rep}: rotated q"
+
+
+def test_lm_bf16_head_group_graph_replays():
+    """The headline's kernel (MHA over bf16 slots, two heads per workgroup)
+    captured once and replayed with new positions and inputs, each replay
+    equal bit for bit to the same call run eagerly."""
+    heads, rows = 8, 12
+    c = W.paged_decode_case(rows, heads, heads, 200, 1500, seed=6, values=None, slack_pages=2)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    qkv = torch.randn(rows, 3 * heads * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    kv = torch.randn(c.num_pages * 16, 2 * heads * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    out = torch.zeros(rows, heads * 128, dtype=torch.bfloat16, device="cuda")
+    pos = dev_i32(np.zeros(rows, np.int32))
+    seq, indptr, pages = dev_i32(np.arange(rows)), dev_i32(c.indptr), dev_i32(c.pages)
+    plan = oa.decode_plan(rows, heads, heads, 16, 1500, 256)
+    plan.group_heads = 2
+    ws = oa.workspace_for(plan)
+
+    def step(s):
+        oa.lm_attend(qkv, kv, pos, seq, 0, indptr, pages, 16, out, heads, 128 ** -0.5, 1200, plan, ws, s)
+
+    rng = np.random.default_rng(9)
+    pos.copy_(dev_i32(_positions(c, rng)[0]))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(s)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step(s)
+    for rep in range(4):
+        pos.copy_(dev_i32(_positions(c, rng)[0]))
+        qkv.copy_(torch.randn(qkv.shape, device="cuda", generator=gen).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        out.zero_()
+        step(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), out.view(torch.int16)), f"replay {rep}: attention output"
