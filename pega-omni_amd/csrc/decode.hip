@@ -290,21 +290,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   merge_waves<G>(a, n, kh, split, nsplit, len, sm_m, sm_l, sm_o);
 }
 
-// ---------------------------------------------------- MHA over bf16 slots
+// ------------------------------------------- K/V head groups over bf16 slots
 //
-// lm_attend's semantics over bf16 slots (one q head per K/V head), with H
-// adjacent heads per workgroup so that every load instruction reads whole
-// contiguous runs of a slot: lane (r, hl, c) = (lane / 16H, lane / 16 % H,
-// lane % 16) owns the 16-byte chunk c of head kg H + hl of key row r, so one
-// load instruction moves R = 4 / H keys x H heads x 256 bytes (H = 4: one key's
-// 1 KB run of four heads' K rows, and of their V rows). A read probe of these
-// patterns over random 16-slot pages of 16 KB slots streams 7.09-7.13 TB/s for
-// four heads over 256 keys per workgroup against 6.77-6.83 TB/s for one head
-// over 1024 (the G = 1 layout of decode_split). Everything else is decode_split's
-// G = 1 path: two register tiles, base-2 online softmax with the scale in q,
-// per-lane V accumulation, waves merged in LDS and splits by decode_combine.
-// The grid is one-dimensional, split index fastest, then head group, then row,
-// so the H-head groups of one row run close together.
+// decode_split's work with H adjacent K/V heads per workgroup, so that every
+// load instruction reads whole contiguous runs of a slot: lane (r, hl, c) =
+// (lane / 16H, lane / 16 % H, lane % 16) owns the 16-byte chunk c of K/V head
+// kh = kg H + hl for key row r, so one load instruction moves R = 4 / H keys x
+// H heads x 256 bytes. Each lane dots its chunk with the G query heads of kh.
+// The plan picks H = 2 for MHA rows (lm_attend's tick over bf16 slots): 505-508
+// us per 128-session layer against 512-515 with one head per workgroup
+// (decode_split<1>), where H = 4 took 526-540. A plan may fix H for GQA rows
+// too (G = 2: slower on the 64-row talker bucket, whose call is short).
+// Everything else is decode_split's: two register tiles for G = 1 and one for
+// G > 1, base-2 online softmax with the scale in q, per-lane V accumulation,
+// waves merged in LDS, splits by decode_combine. The grid is one-dimensional,
+// split index fastest, then head group, then row, so the head groups of one
+// row run close together.
 
 // Combine the R = 4 / H key rows of a wave (lanes 16H apart), per lane.
 template <int H, bool MAX>
