@@ -309,3 +309,28 @@ def test_head_groups_ragged_and_last_page_lengths(oracle, gh):
     torch.cuda.synchronize()
     assert np.array_equal(host_bits(d.out), want)
     assert_close(want, oracle_out(oracle, c), what=f"gh {gh} vs oracle")
+
+
+def test_calls_on_two_streams_overlap_safely(oracle):
+    """Calls are reentrant per stream: two decode problems (one MHA over the
+    head-group kernel, one GQA) issued alternately on two streams, each with
+    its own workspace, equal their serial results bit for bit."""
+    a = W.paged_decode_case(40, 8, 8, 100, 2000, seed=201)
+    b = W.paged_decode_case(24, 16, 8, 100, 2000, seed=202)
+    da, db = DevPaged(a), DevPaged(b)
+    want_a = da.decode(chunk=256, group_heads=2)
+    want_b = db.decode(chunk=256)
+    pa = oa.decode_plan(a.rows, 8, 8, 16, int(a.lens().max()), 256)
+    pa.group_heads = 2
+    pb = oa.decode_plan(b.rows, 16, 8, 16, int(b.lens().max()), 256)
+    wa, wb = oa.workspace_for(pa), oa.workspace_for(pb)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    da.out.zero_(), db.out.zero_()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        oa.qwen3_attend(da.qkv, da.kv, da.pos, da.seq, 0, da.indptr, da.pages, 16, da.out, 8, 8, a.scale, pa, wa, sa)
+        oa.qwen3_attend(db.qkv, db.kv, db.pos, db.seq, 0, db.indptr, db.pages, 16, db.out, 16, 8, b.scale, pb, wb, sb)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_bits(da.out), want_a)
+    assert np.array_equal(host_bits(db.out), want_b)
