@@ -442,13 +442,15 @@ def short_bench(stream, steps, warmup):
     """The small attentions at engine shapes, one launch per step: the code
     predictor's qwen3_attend_dense (64 sessions at position 15 of a 16-slot
     workspace), Mimi's ring attention (128 sessions x 2 rows, 8 heads, full
-    250-slot rings), the codec decoder's fused attention (64 sessions, 16
+    250-slot rings) and the rotary + ring write before it, a 3000-slot prefix
+    copy over FP8 slots, the codec decoder's fused attention (64 sessions, 16
     heads, a full 72-frame ring) and the depformer's last step (128 sessions,
     16 heads, step 7). Bytes: K/V rows read once per (row, head), q, out, writes."""
     import numpy as np
     import torch
 
     import omni_attn as oa
+    import workloads as W
 
     gen = torch.Generator(device="cuda").manual_seed(8)
     i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
@@ -486,6 +488,16 @@ def short_bench(stream, steps, warmup):
     run("mimi_attend", lambda s: oa.mimi_attend(qkv, pos, lines, state, out, sess * T, T, heads, 0.125, ctx, stride,
                                                 s),
         sess * T * heads * (ctx * 256 + 256))
+    # the step before it: Mimi's rotary of q and k, k and v into the ring slots
+    coef = float(np.float32(-np.log(10000.0) * 2.0 / 64))
+    run("mimi_rope_kv", lambda s: oa.mimi_rope_kv(qkv, pos, lines, state, sess * T, T, heads, coef, ctx, stride, s),
+        sess * T * heads * 128 * 6)
+    # PersonaPlex prefix reuse: 3000 FP8 slots of one layer copied to new leases
+    toks = 3000
+    kvc = torch.empty(2 * toks, W.fp8_slot_bytes(32), dtype=torch.uint8, device="cuda")
+    src, dst = i32(np.arange(toks)), i32(toks + np.random.default_rng(0).permutation(toks))
+    run("lm_copy_kv 3000 FP8 slots", lambda s: oa.lm_copy_kv(kvc, src, dst, toks, W.fp8_slot_bytes(32), s),
+        2 * toks * W.fp8_slot_bytes(32))
     # codec decoder: 16 heads of 64, full 72-frame rings
     sess, heads = 64, 16
     width = heads * 64

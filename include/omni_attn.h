@@ -137,6 +137,16 @@ int omni_qwen3_attend_dense(const void* qkv, const void* kv, int per, int base, 
 int omni_mimi_attend(const void* qkv, const int32_t* pos, const int32_t* lines, const void* state, void* out, int rows,
                      int T, int heads, float scale, int context, int64_t stride, void* stream);
 
+/* Replaces `mimi_rope_kv` (crates/omni-personaplex/kernels/mimi.cu:226-246), the
+ * step before mimi_attend, same arguments (the reference's launch:
+ * crates/omni-personaplex/src/mimi.rs:208-223): row n of session s = n / T at
+ * p = pos[s] * T + n % T; its q heads are turned in place by the interleaved
+ * rotary (pair (2i, 2i + 1) by p * exp(i * coef)), its k heads turned into ring
+ * slot p % context (the slot's K heads) and its v heads copied there (the V
+ * heads), each rotated value rounded to bf16. qkv rows [3 heads][64]. */
+int omni_mimi_rope_kv(void* qkv, const int32_t* pos, const int32_t* lines, void* state, int rows, int T, int heads,
+                      float coef, int context, int64_t stride, void* stream);
+
 /* Replaces `codec_attention` (crates/omni-qwen3-tts/kernels/codec.cu:168-277):
  * for session r at p = pos[r], q and k turned by the half-split rotary
  * (pair i = dims i, i + 32, angle p * theta^(-2i/64)) and rounded to bf16; k
@@ -151,6 +161,15 @@ int omni_codec_attention(const void* qkv, const int32_t* pos, const int32_t* lin
  * [seqs][8][K | V][heads * 64] at that step and attends to steps 0 .. step. */
 int omni_lm_dep_kv_attend(const void* qkv, void* ws, int step, void* out, int rows, int heads, float scale,
                           void* stream);
+
+/* Replaces `lm_copy_kv` (crates/omni-personaplex/kernels/lm.cu:583-593; launched per
+ * layer by crates/omni-personaplex/src/helium.rs:166-177 for prefix K/V reuse):
+ * slot dst_slot[r] of one layer's cache takes the bytes of slot src_slot[r],
+ * r < tokens; slot_bytes is a positive multiple of 16 (8448 for the FP8 cache).
+ * A slot that is both a source and a destination of one call gives an
+ * unspecified result, as in the reference. */
+int omni_lm_copy_kv(void* kv, const int32_t* src_slot, const int32_t* dst_slot, int tokens, int slot_bytes,
+                    void* stream);
 
 /* ---------------------------------------------------------- page tables */
 

@@ -30,6 +30,9 @@
  *   oracle_qwen3_attend_dense  crates/omni-qwen3/kernels/qwen3.cu:243-248
  *   oracle_mimi_attend    crates/omni-personaplex/kernels/mimi.cu:248-263 (head 64 ring in
  *                         the session's state, attend_row<64> of attend.cuh:41-106)
+ *   oracle_mimi_rope_kv   crates/omni-personaplex/kernels/mimi.cu:226-246 (rotary of q in
+ *                         place, of k into the ring slot, v copied; rope_head<64>)
+ *   oracle_lm_copy_kv     crates/omni-personaplex/kernels/lm.cu:583-593 (slot copy)
  *   oracle_codec_attention  crates/omni-qwen3-tts/kernels/codec.cu:168-277 (rotary, 72-frame
  *                         ring write and attention, fused)
  *   oracle_lm_dep_kv_attend crates/omni-personaplex/kernels/lm.cu:314-366 (depformer step)
@@ -578,9 +581,9 @@ void oracle_hidream_qk_rope(bf16_t* qkv, int ld, const bf16_t* q_norm, const bf1
   }
 }
 
-/* Interleaved rotation of one head: pair (x[2i], x[2i+1]) by pos * exp(i * coef). */
-static void rope_interleaved(const bf16_t* src, float* out, float pos, float coef) {
-  for (int i = 0; i < HEAD / 2; ++i) {
+/* Interleaved rotation of one head of d dims: pair (x[2i], x[2i+1]) by pos * exp(i * coef). */
+static void rope_interleaved_d(const bf16_t* src, float* out, float pos, float coef, int d) {
+  for (int i = 0; i < d / 2; ++i) {
     const float freq = expf((float)i * coef);
     const float ang = freq * pos;
     const float sn = sinf(ang), cs = cosf(ang);
@@ -588,6 +591,10 @@ static void rope_interleaved(const bf16_t* src, float* out, float pos, float coe
     out[2 * i] = re * cs - im * sn;
     out[2 * i + 1] = re * sn + im * cs;
   }
+}
+
+static void rope_interleaved(const bf16_t* src, float* out, float pos, float coef) {
+  rope_interleaved_d(src, out, pos, coef, HEAD);
 }
 
 static void quantize_head(const float* x, uint8_t* dst, float* scale) {
@@ -629,6 +636,36 @@ void oracle_lm_rope(bf16_t* qkv, const int32_t* pos, const int32_t* slots, uint8
 /* ------------------------------------------------ head-64 ring attentions */
 
 #define D64 64
+
+/* mimi_rope_kv (mimi.cu:226-246 with rope_head<64>, attend.cuh:108-129): row n
+ * of session s = n / T at p = pos[s] * T + n % T; the q heads of qkv row n
+ * [q | k | v][heads][64] turned in place, the k heads turned into ring slot
+ * p % context of the session's state (state + lines[s] * stride bytes, slots
+ * [2 heads][64]: K heads then V heads), the v heads copied there. */
+void oracle_mimi_rope_kv(bf16_t* qkv, const int32_t* pos, const int32_t* lines, uint8_t* state, int rows, int T,
+                         int heads, float coef, int context, int64_t stride) {
+  float x[D64];
+  for (int n = 0; n < rows; ++n) {
+    const int s = n / T;
+    const int p = pos[s] * T + n % T;
+    bf16_t* row = qkv + (int64_t)n * 3 * heads * D64;
+    bf16_t* ring = (bf16_t*)(state + (int64_t)lines[s] * stride);
+    bf16_t* slot = ring + (int64_t)(p % context) * 2 * heads * D64;
+    for (int h = 0; h < 2 * heads; ++h) {
+      rope_interleaved_d(row + (int64_t)h * D64, x, (float)p, coef, D64);
+      bf16_t* dst = h < heads ? row + (int64_t)h * D64 : slot + (int64_t)(h - heads) * D64;
+      for (int i = 0; i < D64; ++i) dst[i] = f2bf(x[i]);
+    }
+    memcpy(slot + (int64_t)heads * D64, row + (int64_t)2 * heads * D64, (size_t)heads * D64 * sizeof(bf16_t));
+  }
+}
+
+/* lm_copy_kv (lm.cu:583-593): slot dst_slot[r] of one layer's cache takes the
+ * bytes of slot src_slot[r], for r < tokens (prefix K/V reuse). */
+void oracle_lm_copy_kv(uint8_t* kv, const int32_t* src_slot, const int32_t* dst_slot, int tokens, int slot_bytes) {
+  for (int r = 0; r < tokens; ++r)
+    memmove(kv + (int64_t)dst_slot[r] * slot_bytes, kv + (int64_t)src_slot[r] * slot_bytes, (size_t)slot_bytes);
+}
 
 /* attend_row<64> (attend.cuh:41-106) for one (row, head): q (64 f32), keys
  * t = 0 .. len-1 with K row krow(t) and V row vrow(t); 4 warps x 32-key tiles,

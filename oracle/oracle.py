@@ -17,6 +17,8 @@ the pega-omni tree):
 * :func:`qwen3_rope` / :func:`qwen3_rope_dense` — ``qwen3.cu:64-111``.
 * :func:`qwen3_attend_dense` — ``qwen3.cu:243-248``.
 * :func:`mimi_attend` — ``crates/omni-personaplex/kernels/mimi.cu:248-263``.
+* :func:`mimi_rope_kv` — ``crates/omni-personaplex/kernels/mimi.cu:226-246``.
+* :func:`lm_copy_kv` — ``crates/omni-personaplex/kernels/lm.cu:583-593``.
 * :func:`codec_attention` — ``crates/omni-qwen3-tts/kernels/codec.cu:168-277``.
 * :func:`lm_dep_kv_attend` — ``crates/omni-personaplex/kernels/lm.cu:314-366``.
 * :func:`hidream_qk_rope` — ``crates/omni-hidream-o1/kernels/hidream.cu:55-106``.
@@ -70,6 +72,10 @@ def lib():
         L.oracle_qwen3_attend_dense.restype = i32
         L.oracle_mimi_attend.argtypes = [P, P, P, P, P, i32, i32, i32, f32, i32, i64]
         L.oracle_mimi_attend.restype = None
+        L.oracle_mimi_rope_kv.argtypes = [P, P, P, P, i32, i32, i32, f32, i32, i64]
+        L.oracle_mimi_rope_kv.restype = None
+        L.oracle_lm_copy_kv.argtypes = [P, P, P, i32, i32]
+        L.oracle_lm_copy_kv.restype = None
         L.oracle_codec_attention.argtypes = [P, P, P, P, P, i32, i64, i32, f32]
         L.oracle_codec_attention.restype = None
         L.oracle_lm_dep_kv_attend.argtypes = [P, P, i32, P, i32, i32, f32]
@@ -216,6 +222,24 @@ def mimi_attend(qkv, pos, lines, state, rows, T, heads, scale, context, stride):
     lib().oracle_mimi_attend(_p(qkv), _p(pos), _p(lines), _p(state), _p(out), rows, T, heads, float(scale), context,
                              int(stride))
     return out
+
+
+def mimi_rope_kv(qkv, pos, lines, state, rows, T, heads, coef, context, stride):
+    """Returns (qkv', state'): q rotated in place, k rotated and v copied into
+    each row's ring slot."""
+    qkv, state = qkv.copy(), state.copy()
+    lib().oracle_mimi_rope_kv(_p(qkv), _p(pos), _p(lines), _p(state), rows, T, heads, float(coef), context,
+                              int(stride))
+    return qkv, state
+
+
+def lm_copy_kv(kv, src_slot, dst_slot, slot_bytes):
+    """kv: uint8 [slots][slot_bytes]. Returns the cache after the copies."""
+    kv = np.ascontiguousarray(kv).copy()
+    src = np.ascontiguousarray(src_slot, dtype=np.int32)
+    dst = np.ascontiguousarray(dst_slot, dtype=np.int32)
+    lib().oracle_lm_copy_kv(_p(kv), _p(src), _p(dst), len(src), int(slot_bytes))
+    return kv
 
 
 def codec_attention(qkv, pos, lines, kv, rows, stride, heads, theta):

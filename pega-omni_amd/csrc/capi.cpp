@@ -674,6 +674,44 @@ int omni_mimi_attend(const void* qkv, const int32_t* pos, const int32_t* lines, 
   return short_common(a, omni::kShortMimi, "mimi_attend", stream);
 }
 
+int omni_mimi_rope_kv(void* qkv, const int32_t* pos, const int32_t* lines, void* state, int rows, int T, int heads,
+                      float coef, int context, int64_t stride, void* stream) {
+  if (rows < 0 || heads <= 0) return fail(OMNI_ATTN_EINVAL, "mimi_rope_kv: rows=%d heads=%d", rows, heads);
+  if (rows == 0) return ok();
+  if (!qkv || !pos || !lines || !state || !aligned16(qkv) || !aligned16(state))
+    return fail(OMNI_ATTN_EINVAL, "mimi_rope_kv: qkv and state must be 16-byte aligned device pointers");
+  if (T <= 0 || context <= 0 || stride % 16 != 0 || !std::isfinite(coef) || heads > 4096)
+    return fail(OMNI_ATTN_EINVAL, "mimi_rope_kv: T=%d context=%d stride=%lld heads=%d", T, context, (long long)stride,
+                heads);
+  omni::ShortArgs a{};
+  a.qkv_rw = static_cast<omni::bf16_t*>(qkv);
+  a.pos = pos;
+  a.lines = lines;
+  a.state = state;
+  a.stride = stride;
+  a.rows = rows;
+  a.heads = heads;
+  a.T = T;
+  a.context = context;
+  a.coef = coef;
+  if (omni::launch_short(a, omni::kShortMimiRope, as_stream(stream)) != 0)
+    return fail(OMNI_ATTN_ELAUNCH, "mimi_rope_kv: launch failed: %s", hipGetErrorString(omni::g_launch_status));
+  return ok();
+}
+
+int omni_lm_copy_kv(void* kv, const int32_t* src_slot, const int32_t* dst_slot, int tokens, int slot_bytes,
+                    void* stream) {
+  if (tokens < 0 || slot_bytes <= 0 || slot_bytes % 16 != 0)
+    return fail(OMNI_ATTN_EINVAL, "lm_copy_kv: tokens=%d slot_bytes=%d (a positive multiple of 16)", tokens,
+                slot_bytes);
+  if (tokens == 0) return ok();
+  if (!kv || !src_slot || !dst_slot || !aligned16(kv))
+    return fail(OMNI_ATTN_EINVAL, "lm_copy_kv: kv must be a 16-byte aligned device pointer");
+  if (omni::launch_copy_slots(kv, src_slot, dst_slot, tokens, slot_bytes, as_stream(stream)) != 0)
+    return fail(OMNI_ATTN_ELAUNCH, "lm_copy_kv: launch failed: %s", hipGetErrorString(omni::g_launch_status));
+  return ok();
+}
+
 int omni_codec_attention(const void* qkv, const int32_t* pos, const int32_t* lines, void* kv, void* out, int rows,
                          int64_t stride, int heads, float theta, void* stream) {
   if (rows > 0) {

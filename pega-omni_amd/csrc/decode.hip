@@ -909,6 +909,26 @@ int noalloc_scratch(float** ptr) {
   return 0;
 }
 
+// ------------------------------------------------------------- slot copies
+
+// lm_copy_kv (crates/omni-personaplex/kernels/lm.cu:583-593): slot dst[r] of
+// one layer's cache takes the bytes of slot src[r]. A workgroup per copied
+// slot, 16-byte words, slot_bytes a multiple of 16.
+__global__ __launch_bounds__(256) void copy_slots_kernel(uint8_t* kv, const int32_t* src, const int32_t* dst,
+                                                         int slot_bytes) {
+  const int r = blockIdx.x;
+  const uint4* from = reinterpret_cast<const uint4*>(kv + (int64_t)src[r] * slot_bytes);
+  uint4* to = reinterpret_cast<uint4*>(kv + (int64_t)dst[r] * slot_bytes);
+  for (int i = threadIdx.x; i < slot_bytes / 16; i += 256) to[i] = from[i];
+}
+
+int launch_copy_slots(void* kv, const int32_t* src, const int32_t* dst, int tokens, int slot_bytes,
+                      hipStream_t stream) {
+  if (tokens == 0) return 0;
+  copy_slots_kernel<<<tokens, 256, 0, stream>>>(static_cast<uint8_t*>(kv), src, dst, slot_bytes);
+  return check_launch();
+}
+
 // ------------------------------------------------------------------ gather
 
 // Block per sequence i: copy its first lens[i] tokens' slots to dense rows.

@@ -37,7 +37,7 @@ struct DecodeArgs {
   float scale_log2;  // softmax scale times log2(e)
   int fp8;           // 1: kv slots are FP8 E4M3 with f32 scales (lm_attend's cache)
   int64_t slot_bytes;  // bytes per FP8 slot: 2 hk 128 + 2 hk 4
-  int group_heads;     // FP8: heads per workgroup (0 = pick from the shape)
+  int group_heads;     // K/V heads per workgroup of the head-group kernels (0 = pick from the shape)
   int dense_per, dense_base, dense_span;  // dense rows (len_mode 2): slot (n / per) * span + t
 };
 
@@ -50,6 +50,10 @@ constexpr int kMaxDevices = 64;
 // Device address of that array on the current device (looked up once per
 // device); 0 on success, -1 if the lookup fails.
 int noalloc_scratch(float** ptr);
+
+// Copy of whole cache slots (prefix K/V reuse): slot dst[r] takes slot src[r].
+int launch_copy_slots(void* kv, const int32_t* src, const int32_t* dst, int tokens, int slot_bytes,
+                      hipStream_t stream);
 
 int launch_gather_kv(const void* kv, int hk, const int32_t* indptr, const int32_t* pages, PageDiv pd,
                      const int32_t* seq_ids, const int32_t* lens, const int32_t* out_indptr, int nseq, void* out,
@@ -126,10 +130,12 @@ struct ShortArgs {
   int64_t stride;
   bf16_t* ws;            // depformer workspace [seqs][8][K | V][heads * 64]
   bf16_t* out;
+  bf16_t* qkv_rw;        // Mimi rotary: the qkv rows, q turned in place
   int rows, heads, T, context, step;
   float scale, theta;
+  float coef;            // Mimi rotary: pair i turns by p * exp(i * coef)
 };
-constexpr int kShortMimi = 0, kShortCodec = 1, kShortDep = 2;
+constexpr int kShortMimi = 0, kShortCodec = 1, kShortDep = 2, kShortMimiRope = 3;
 int launch_short(const ShortArgs& a, int kind, hipStream_t stream);
 
 constexpr int kRopeQwen3 = 0, kRopeQwen3Dense = 1, kRopeHidream = 2, kRopeLm = 3;

@@ -1,8 +1,9 @@
 // Head-64 attentions over short rings (gfx950, wave64): the Mimi codec
-// transformer's ring attention, the Qwen3-TTS codec decoder's fused
-// rotary + ring write + attention, and the PersonaPlex depformer's fused K/V
-// write + causal attention.
+// transformer's ring attention and the rotary + ring write before it, the
+// Qwen3-TTS codec decoder's fused rotary + ring write + attention, and the
+// PersonaPlex depformer's fused K/V write + causal attention.
 //
+//   mimi_rope_kv64      crates/omni-personaplex/kernels/mimi.cu:226-246
 //   mimi_attend64       crates/omni-personaplex/kernels/mimi.cu:248-263
 //   codec_attention64   crates/omni-qwen3-tts/kernels/codec.cu:168-277
 //   dep_kv_attend64     crates/omni-personaplex/kernels/lm.cu:314-366
@@ -154,6 +155,45 @@ __global__ __launch_bounds__(64) void mimi_attend64(ShortArgs a) {
   st.finish(a.out + ((int64_t)n * a.heads + h) * kD);
 }
 
+// Mimi's rotary + ring write: row n of session s = n / T at p = pos[s] T +
+// n % T. One 256-thread workgroup per row; the row's 32 angles (pair i turns
+// by p exp(i coef), computed with expf and sincosf as the reference does) go
+// to LDS once. Thread u takes the 16-byte chunk u % 8 (dims 8c .. 8c + 7,
+// interleaved pairs 4c .. 4c + 3) of head u / 8 of [q | k | v]: q heads are
+// turned in place, k heads turned into ring slot p % context (its K heads),
+// v heads copied there (its V heads), each rotated value rounded to bf16.
+__global__ __launch_bounds__(256) void mimi_rope_kv64(ShortArgs a) {
+  const int n = blockIdx.x, s = n / a.T;
+  const int p = a.pos[s] * a.T + n % a.T;
+  __shared__ float s_cos[kD / 2], s_sin[kD / 2];
+  if (threadIdx.x < kD / 2) {
+    const float freq = expf((float)threadIdx.x * a.coef);
+    sincosf(freq * (float)p, &s_sin[threadIdx.x], &s_cos[threadIdx.x]);
+  }
+  __syncthreads();
+  bf16_t* row = a.qkv_rw + (int64_t)n * 3 * a.heads * kD;
+  bf16_t* slot = reinterpret_cast<bf16_t*>(static_cast<uint8_t*>(a.state) + (int64_t)a.lines[s] * a.stride) +
+                 (int64_t)(p % a.context) * 2 * a.heads * kD;
+  for (int u = threadIdx.x; u < 3 * a.heads * 8; u += blockDim.x) {
+    const int hh = u >> 3, c = u & 7;
+    const uint4 w = ldg16(row + hh * kD + 8 * c);
+    if (hh >= 2 * a.heads) {  // v: copied into the slot's V heads
+      *reinterpret_cast<uint4*>(slot + (int64_t)(hh - a.heads) * kD + 8 * c) = w;
+      continue;
+    }
+    float x[8], y[8];
+    widen8(w, x);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float cs = s_cos[4 * c + j], sn = s_sin[4 * c + j];
+      y[2 * j] = x[2 * j] * cs - x[2 * j + 1] * sn;
+      y[2 * j + 1] = x[2 * j] * sn + x[2 * j + 1] * cs;
+    }
+    bf16_t* dst = hh < a.heads ? row + hh * kD : slot + (int64_t)(hh - a.heads) * kD;
+    *reinterpret_cast<uint4*>(dst + 8 * c) = pack8(y);
+  }
+}
+
 // ------------------------------------------------------ Qwen3-TTS codec ring
 struct CodecRing {
   const bf16_t* ring;  // K[72][width] then V[72][width]
@@ -250,6 +290,7 @@ int launch_short(const ShortArgs& a, int kind, hipStream_t stream) {
     case kShortMimi: mimi_attend64<<<grid, 64, 0, stream>>>(a); break;
     case kShortCodec: codec_attention64<<<grid, 64, 0, stream>>>(a); break;
     case kShortDep: dep_kv_attend64<<<grid, 64, 0, stream>>>(a); break;
+    case kShortMimiRope: mimi_rope_kv64<<<a.rows, 256, 0, stream>>>(a); break;
     default: return -2;
   }
   return check_launch();

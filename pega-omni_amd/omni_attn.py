@@ -43,6 +43,8 @@ EXPORTS = (
     "omni_hidream_workspace_bytes",
     "omni_qwen3_attend_dense",
     "omni_mimi_attend",
+    "omni_mimi_rope_kv",
+    "omni_lm_copy_kv",
     "omni_codec_attention",
     "omni_lm_dep_kv_attend",
     "omni_qwen3_rope",
@@ -132,6 +134,8 @@ def load(path: str | None = None):
         "omni_hidream_workspace_bytes": [],
         "omni_qwen3_attend_dense": [P, P, i32, i32, i32, P, i32, i32, f32, dplan, P, P],
         "omni_mimi_attend": [P, P, P, P, P, i32, i32, i32, f32, i32, i64, P],
+        "omni_mimi_rope_kv": [P, P, P, P, i32, i32, i32, f32, i32, i64, P],
+        "omni_lm_copy_kv": [P, P, P, i32, i32, P],
         "omni_codec_attention": [P, P, P, P, P, i32, i64, i32, f32, P],
         "omni_lm_dep_kv_attend": [P, P, i32, P, i32, i32, f32, P],
         "omni_qwen3_rope": [P, P, P, P, P, P, i32, i32, i32, f32, f32, P],
@@ -417,6 +421,23 @@ def qwen3_attend_dense(qkv, kv, per, base, span, out, hq, hk, scale, plan, works
     _check(load().omni_qwen3_attend_dense(_ptr(qkv), _ptr(kv), per, base, span, _ptr(out), hq, hk, float(scale),
                                           ctypes.byref(plan), _ws(plan, workspace), _stream(stream)))
     return out
+
+
+def mimi_rope_kv(qkv, pos, lines, state, rows, T, heads, coef, context, stride, stream=None):
+    """``mimi_rope_kv`` (crates/omni-personaplex/kernels/mimi.cu:226-246): q turned
+    in place, k turned and v copied into each row's ring slot of ``state``."""
+    _bf16_dev(qkv, "qkv"), _i32_dev(pos, "pos"), _i32_dev(lines, "lines")
+    _check(load().omni_mimi_rope_kv(_ptr(qkv), _ptr(pos), _ptr(lines), _ptr(state), rows, T, heads, float(coef),
+                                    context, int(stride), _stream(stream)))
+    return qkv
+
+
+def lm_copy_kv(kv, src_slot, dst_slot, tokens, slot_bytes, stream=None):
+    """``lm_copy_kv`` (crates/omni-personaplex/kernels/lm.cu:583-593): slot
+    dst_slot[r] takes the bytes of slot src_slot[r] (prefix K/V reuse)."""
+    _i32_dev(src_slot, "src_slot"), _i32_dev(dst_slot, "dst_slot")
+    _check(load().omni_lm_copy_kv(_ptr(kv), _ptr(src_slot), _ptr(dst_slot), tokens, slot_bytes, _stream(stream)))
+    return kv
 
 
 def mimi_attend(qkv, pos, lines, state, out, rows, T, heads, scale, context, stride, stream=None):

@@ -267,6 +267,10 @@ static void check_head64_validation(void) {
   CHECK(omni_hidream_qk_rope(kFake, 48 * 128, kFake, kFake, kFake, kFake, kFake, kFake, 4, 32, 8, 22, 1e-6f, 5e6f,
                              NULL) == OMNI_ATTN_EINVAL);
   CHECK(omni_attn_gather_kv(kFake, 8, kFake, kFake, 0, kFake, kFake, kFake, 2, kFake, NULL) == OMNI_ATTN_EINVAL);
+  CHECK(omni_mimi_rope_kv(kFake, kFake, kFake, kFake, 4, 0, 8, -0.28f, 250, 64000, NULL) == OMNI_ATTN_EINVAL);
+  CHECK(omni_mimi_rope_kv(kFake, kFake, kFake, kFake, 0, 2, 8, -0.28f, 250, 64000, NULL) == OMNI_ATTN_OK);
+  CHECK(omni_lm_copy_kv(kFake, kFake, kFake, 3, 8440, NULL) == OMNI_ATTN_EINVAL);
+  CHECK(omni_lm_copy_kv(NULL, NULL, NULL, 0, 8448, NULL) == OMNI_ATTN_OK);
 }
 
 int main(void) {

@@ -349,3 +349,22 @@ def test_empty_batches_return_before_any_launch():
                                        ctypes.byref(plan))
     assert rc == oa.OK and plan.tiles == 0
     assert L.omni_attn_prefill_run(ctypes.byref(plan), f, f, f, f, f, f, f, 0.1, f, None) == oa.OK
+
+
+def test_mimi_rope_kv_and_copy_kv_validate_before_launch():
+    """The two cache writers refuse bad shapes on any host, GPU or not."""
+    L = oa.load()
+    f, odd = ctypes.c_void_p(4096), ctypes.c_void_p(4100)
+    coef = -0.28
+    assert L.omni_mimi_rope_kv(f, f, f, f, 0, 2, 8, coef, 250, 64000, None) == oa.OK  # no rows: nothing to do
+    assert L.omni_mimi_rope_kv(f, f, f, f, 4, 0, 8, coef, 250, 64000, None) == oa.EINVAL  # T
+    assert L.omni_mimi_rope_kv(f, f, f, f, 4, 2, 8, coef, 0, 64000, None) == oa.EINVAL  # context
+    assert L.omni_mimi_rope_kv(f, f, f, f, 4, 2, 8, coef, 250, 64008, None) == oa.EINVAL  # stride % 16
+    assert L.omni_mimi_rope_kv(odd, f, f, f, 4, 2, 8, coef, 250, 64000, None) == oa.EINVAL  # alignment
+    assert L.omni_mimi_rope_kv(f, f, f, f, 4, 2, 0, coef, 250, 64000, None) == oa.EINVAL  # heads
+    assert L.omni_mimi_rope_kv(f, f, f, f, 4, 2, 8, float("nan"), 250, 64000, None) == oa.EINVAL
+    assert L.omni_lm_copy_kv(None, None, None, 0, 8448, None) == oa.OK
+    assert L.omni_lm_copy_kv(f, f, f, 3, 8440, None) == oa.EINVAL  # not a multiple of 16
+    assert L.omni_lm_copy_kv(f, f, f, -1, 8448, None) == oa.EINVAL
+    assert L.omni_lm_copy_kv(odd, f, f, 3, 8448, None) == oa.EINVAL
+    assert L.omni_lm_copy_kv(f, None, f, 3, 8448, None) == oa.EINVAL

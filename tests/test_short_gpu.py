@@ -89,3 +89,71 @@ def test_lm_dep_kv_attend(oracle, step):
     torch.cuda.synchronize()
     assert np.array_equal(host_bits(d_ws), ws_want)
     assert_close(host_bits(out), want, what="lm_dep_kv_attend")
+
+
+def _interleaved_bound(x, p):
+    """One bf16 ulp plus (2^-22 + p 2^-21) of each interleaved pair's
+    magnitude: device and host sin/cos and exp may round apart by that much."""
+    m = np.maximum(np.abs(x[..., 0::2]), np.abs(x[..., 1::2]))
+    return np.repeat(m, 2, axis=-1) * (2.0 ** -22 + p * 2.0 ** -21)
+
+
+@pytest.mark.parametrize("seed,context,pos_hi,sessions,T", [(7, 40, 60, 3, 2), (8, 250, 3000, 128, 2), (9, 16, 5, 2, 1)])
+def test_mimi_rope_kv(oracle, seed, context, pos_hi, sessions, T):
+    """Mimi's rotary + ring write against the oracle: rotated q (in place) and
+    k (ring slot) to the rotary rounding bound, v bit-exact, every other byte
+    of qkv and of the state untouched; then mimi_attend over the written rings
+    against the oracle's chain."""
+    c = mimi_case(seed, sessions=sessions, T=T, heads=8, context=context, pos_hi=pos_hi)
+    heads, rows = c["heads"], c["rows"]
+    coef = float(np.float32(-np.log(10000.0) * 2.0 / 64))
+    q_want, st_want = oracle.mimi_rope_kv(c["qkv"], c["pos"], c["lines"], c["state"], rows, T, heads, coef,
+                                          c["context"], c["stride"])
+    qkv = dev_bits(c["qkv"])
+    state = torch.from_numpy(c["state"]).cuda()
+    oa.mimi_rope_kv(qkv, dev_i32(c["pos"]), dev_i32(c["lines"]), state, rows, T, heads, coef, c["context"],
+                    c["stride"])
+    torch.cuda.synchronize()
+    q_got, st_got = host_bits(qkv), state.cpu().numpy()
+    p = np.array([int(c["pos"][n // T]) * T + n % T for n in range(rows)], np.float64)
+    x = bits_to_f64(c["qkv"]).reshape(rows, 3 * heads, 64)
+    g = bits_to_f64(q_got).reshape(rows, 3 * heads, 64)
+    w = bits_to_f64(q_want).reshape(rows, 3 * heads, 64)
+    b = bf16_ulp(w[:, :heads]) * 1.0001 + _interleaved_bound(x[:, :heads], p[:, None, None])
+    assert np.all(np.abs(g[:, :heads] - w[:, :heads]) <= b), "rotated q"
+    assert np.array_equal(q_got.reshape(rows, 3, -1)[:, 1:], c["qkv"].reshape(rows, 3, -1)[:, 1:])
+    slot_bytes = 2 * heads * 64 * 2
+    diff = st_got != st_want
+    for n in range(rows):
+        at = int(c["lines"][n // T]) * c["stride"] + (int(p[n]) % c["context"]) * slot_bytes
+        gs = bits_to_f64(st_got[at:at + slot_bytes].view(np.uint16)).reshape(2 * heads, 64)
+        ws = bits_to_f64(st_want[at:at + slot_bytes].view(np.uint16)).reshape(2 * heads, 64)
+        bk = bf16_ulp(ws[:heads]) * 1.0001 + _interleaved_bound(x[n, heads:2 * heads], p[n])
+        assert np.all(np.abs(gs[:heads] - ws[:heads]) <= bk), f"rotated k, row {n}"
+        assert np.array_equal(gs[heads:], ws[heads:]), f"v, row {n}"
+        diff[at:at + slot_bytes // 2] = False
+    assert not diff.any(), "bytes outside the rotated K heads differ"
+    # The chain: attention over the rings just written, from the rotated q.
+    out = torch.zeros(rows, heads * 64, dtype=torch.bfloat16, device="cuda")
+    oa.mimi_attend(qkv, dev_i32(c["pos"]), dev_i32(c["lines"]), state, out, rows, T, heads, 0.125, c["context"],
+                   c["stride"])
+    torch.cuda.synchronize()
+    want = oracle.mimi_attend(q_want, c["pos"], c["lines"], st_want, rows, T, heads, 0.125, c["context"],
+                              c["stride"])
+    assert_close(host_bits(out), want, what="mimi_rope_kv -> mimi_attend")
+
+
+@pytest.mark.parametrize("slot_bytes,tokens", [(8448, 300), (16384, 64), (8448, 0), (16, 5)])
+def test_lm_copy_kv(oracle, slot_bytes, tokens):
+    """Prefix K/V reuse: slot dst[r] takes slot src[r]'s bytes, bit for bit,
+    everything else untouched (FP8 slots of 8448 bytes, bf16 slots of 16 KiB)."""
+    rng = np.random.default_rng(slot_bytes + tokens)
+    slots = 2 * tokens + 17
+    kv = rng.integers(0, 256, size=(slots, slot_bytes), dtype=np.uint8)
+    perm = rng.permutation(slots).astype(np.int32)
+    src, dst = perm[:tokens], perm[tokens:2 * tokens]
+    d_kv = torch.from_numpy(kv).cuda()
+    oa.lm_copy_kv(d_kv, dev_i32(src), dev_i32(dst), tokens, slot_bytes)
+    torch.cuda.synchronize()
+    want = oracle.lm_copy_kv(kv, src, dst, slot_bytes)
+    assert np.array_equal(d_kv.cpu().numpy(), want)

@@ -166,3 +166,63 @@ def test_lm_dep_kv_attend(oracle, step):
         for h in range(heads):
             want[s, h] = sdpa(bits_to_f64(x[s, 0, h]), wf[s, : step + 1, 0, h], wf[s, : step + 1, 1, h], 0.125)
     assert_ulp(out, want, "dep")
+
+
+def _helium64(x, pos):
+    """[rows][heads][64] float64 turned at pos[rows] by transformers' Helium
+    rotary (interleaved pairs (2i, 2i + 1), theta 10000) at head_dim 64."""
+    from transformers import HeliumConfig
+    from transformers.models.helium import modeling_helium as helium
+    cfg = HeliumConfig(head_dim=64, hidden_size=512, num_attention_heads=8, num_key_value_heads=8, rope_theta=10000.0)
+    rot = helium.HeliumRotaryEmbedding(cfg)
+    xt = torch.from_numpy(x).permute(1, 0, 2)[None]
+    cos, sin = rot(xt, torch.from_numpy(pos.astype(np.int64))[None])
+    return helium.apply_rotary_pos_emb(xt, xt, cos, sin)[0][0].permute(1, 0, 2).numpy()
+
+
+@pytest.mark.parametrize("seed,context,pos_hi", [(4, 40, 60), (5, 250, 3000)])
+def test_mimi_rope_kv_matches_helium_rotary(oracle, seed, context, pos_hi):
+    """mimi_rope_kv: q turned in place and k turned into ring slot p % context
+    by the interleaved rotary (against transformers' Helium rotary at head_dim
+    64, to 2^-7 of each pair's magnitude: the oracle rounds its output), v
+    copied bit for bit; every other byte of the state and of qkv unchanged."""
+    c = mimi_case(seed, context=context, pos_hi=pos_hi)
+    heads, T, rows = c["heads"], c["T"], c["rows"]
+    coef = float(np.float32(-np.log(10000.0) * 2.0 / 64))
+    q2, st2 = oracle.mimi_rope_kv(c["qkv"], c["pos"], c["lines"], c["state"], rows, T, heads, coef, c["context"],
+                                  c["stride"])
+    x = bits_to_f64(c["qkv"]).reshape(rows, 3 * heads, 64)
+    p = np.array([int(c["pos"][n // T]) * T + n % T for n in range(rows)])
+
+    def bound(xn):
+        m = np.maximum(np.abs(xn[..., 0::2]), np.abs(xn[..., 1::2]))
+        return 2.0 ** -7 * np.repeat(m, 2, axis=-1) + 1e-30
+
+    q_got = bits_to_f64(q2).reshape(rows, 3 * heads, 64)
+    assert np.all(np.abs(q_got[:, :heads] - _helium64(x[:, :heads], p)) <= bound(x[:, :heads]))
+    assert np.array_equal(q2.reshape(rows, 3, -1)[:, 1:], c["qkv"].reshape(rows, 3, -1)[:, 1:])
+    k_want = _helium64(x[:, heads:2 * heads], p)
+    touched = np.zeros(len(c["state"]), bool)
+    slot_bytes = 2 * heads * 64 * 2
+    for n in range(rows):
+        s = n // T
+        at = int(c["lines"][s]) * c["stride"] + (p[n] % c["context"]) * slot_bytes
+        slot = st2[at:at + slot_bytes].view(np.uint16).reshape(2 * heads, 64)
+        assert np.all(np.abs(bits_to_f64(slot[:heads]) - k_want[n]) <= bound(x[n, heads:2 * heads]))
+        assert np.array_equal(slot[heads:], c["qkv"][n].reshape(3 * heads, 64)[2 * heads:])
+        touched[at:at + slot_bytes] = True
+    assert np.array_equal(st2[~touched], c["state"][~touched])
+
+
+def test_lm_copy_kv_is_slot_indexing(oracle):
+    """lm_copy_kv: slot dst[r] takes slot src[r]'s bytes (FP8 slots of 8448
+    bytes), the rest of the cache unchanged; equal to numpy's indexing."""
+    rng = np.random.default_rng(6)
+    slots, sb = 300, 8448
+    kv = rng.integers(0, 256, size=(slots, sb), dtype=np.uint8)
+    perm = rng.permutation(slots)
+    src, dst = perm[:40].astype(np.int32), perm[40:80].astype(np.int32)
+    got = oracle.lm_copy_kv(kv, src, dst, sb)
+    want = kv.copy()
+    want[dst] = kv[src]
+    assert np.array_equal(got, want)
