@@ -253,6 +253,21 @@ int omni_hidream_attend_batched(const void* q, const void* k, const void* v, voi
 int omni_qwen3_rope(void* qkv, const void* q_norm, const void* k_norm, const int32_t* pos, const int32_t* slots,
                     void* kv, int rows, int hq, int hk, float eps, float theta, void* stream);
 
+/* omni_qwen3_rope followed by omni_qwen3_attend on decode rows (ragged = 0:
+ * row n is sequence n and attends to pos[n] + 1 keys), in one launch; it has
+ * no counterpart in the reference, which runs the two as separate launches
+ * (crates/omni-qwen3/src/stack.rs:222-240). The output and the K and V
+ * written to slot slots[n] are bit-identical to the two calls'. Differences:
+ * q is rotated in registers only (qkv is not written), and key pos[n] of row
+ * n is taken from the rotated row, so slots[n] must be the slot the page
+ * table gives key pos[n] (what the engines' Rows builder produces), and no
+ * other row of the call may read slots[n]. The plan is a decode plan
+ * (group_heads 0 or 1). */
+int omni_qwen3_rope_attend(const void* qkv, const void* q_norm, const void* k_norm, const int32_t* pos,
+                           const int32_t* slots, void* kv, const int32_t* indptr, const int32_t* pages, int page,
+                           void* out, int hq, int hk, float eps, float theta, float scale,
+                           const omni_attn_decode_plan* plan, void* workspace, void* stream);
+
 /* Replaces `qwen3_rope_dense` (qwen3.cu:105-111): `per` consecutive rows per
  * sequence at positions base, base + 1, ..., slot seq * span + pos of a dense
  * workspace (base + per <= span). */

@@ -57,7 +57,8 @@ int pick_chunk(int rows, int hk, int max_len) {
 int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int32_t* seq, int ragged,
                   const int32_t* indptr, const int32_t* pages, int page, void* out, int hq, int hk, float scale,
                   int context, int len_mode, const omni_attn_decode_plan* plan, void* workspace, void* stream,
-                  int fp8 = 0, int dense_per = 0, int dense_base = 0, int dense_span = 0) {
+                  int fp8 = 0, int dense_per = 0, int dense_base = 0, int dense_span = 0,
+                  const omni::DecodeArgs* rope = nullptr) {
   if (!plan) return fail(OMNI_ATTN_EINVAL, "decode: null plan");
   if (plan->hq != hq || plan->hk != hk || plan->page != page)
     return fail(OMNI_ATTN_EINVAL, "decode: plan was made for hq=%d hk=%d page=%d, called with hq=%d hk=%d page=%d",
@@ -116,6 +117,15 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
   a.dense_per = dense_per;
   a.dense_base = dense_base;
   a.dense_span = dense_span;
+  if (rope) {
+    a.rope = 1;
+    a.q_norm = rope->q_norm;
+    a.k_norm = rope->k_norm;
+    a.slots = rope->slots;
+    a.kv_w = rope->kv_w;
+    a.eps = rope->eps;
+    a.theta = rope->theta;
+  }
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
   if (rc == -2)
     return fail(OMNI_ATTN_EUNSUPPORTED, "decode: hq/hk=%d and group_heads=%d not served, or the grid passes 2^31 "
@@ -622,6 +632,28 @@ int omni_hidream_qk_rope(void* qkv, int ld, const void* q_norm, const void* k_no
   a.eps = eps;
   a.theta = theta;
   return rope_common(a, omni::kRopeHidream, "hidream_qk_rope", stream);
+}
+
+int omni_qwen3_rope_attend(const void* qkv, const void* q_norm, const void* k_norm, const int32_t* pos,
+                           const int32_t* slots, void* kv, const int32_t* indptr, const int32_t* pages, int page,
+                           void* out, int hq, int hk, float eps, float theta, float scale,
+                           const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  if (plan && plan->rows > 0) {
+    if (int rc = norm_rope_checks(q_norm, k_norm, eps, theta, "qwen3_rope_attend")) return rc;
+    if (!slots) return fail(OMNI_ATTN_EINVAL, "qwen3_rope_attend: null slots");
+    if (plan->group_heads > 1)
+      return fail(OMNI_ATTN_EINVAL, "qwen3_rope_attend: plan group_heads=%d (the fused kernel takes one K/V head per "
+                  "workgroup: 0 or 1)", plan->group_heads);
+  }
+  omni::DecodeArgs r{};
+  r.q_norm = static_cast<const omni::bf16_t*>(q_norm);
+  r.k_norm = static_cast<const omni::bf16_t*>(k_norm);
+  r.slots = slots;
+  r.kv_w = static_cast<omni::bf16_t*>(kv);
+  r.eps = eps;
+  r.theta = theta;
+  return decode_common(qkv, kv, pos, nullptr, 0, indptr, pages, page, out, hq, hk, scale, 0, 0, plan, workspace,
+                       stream, 0, 0, 0, 0, &r);
 }
 
 int omni_qwen3_attend_dense(const void* qkv, const void* kv, int per, int base, int span, void* out, int hq, int hk,

@@ -25,6 +25,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "rotary.h"
 
 namespace omni {
 
@@ -101,7 +102,15 @@ __device__ __forceinline__ int64_t key_slot(const PageDiv& d, int pid, int t) {
   return DIV ? page_slot(d, pid, t) : (((int64_t)pid << d.shift) | (t & ((1 << d.shift) - 1)));
 }
 
-template <int G, int SLOTS, bool DIV>
+// ROPE: the fused Qwen3 rotary (omni_qwen3_rope_attend), decode rows only
+// (each row its own sequence, len = pos[n] + 1, so the row's new key is its
+// last). Every workgroup of the row turns its G q heads itself, as qwen3_rope
+// would have (RMSNorm, rotary, bf16 rounding), from the row's angle table in
+// LDS. The one split holding key pos[n] also turns the row's k head kh,
+// writes K and V into slot slots[n], and in the tile that holds key pos[n]
+// replaces the loaded K and V of that key (which may predate the write) by
+// the values in its registers.
+template <int G, int SLOTS, bool DIV, bool ROPE>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   const int kh = blockIdx.y, n = blockIdx.z;
   const int split = rotated_split(blockIdx.x, kh + a.hk * n, a.splits);
@@ -119,16 +128,58 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
 
   float q[G][8];
   const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * G * kHead + c * 8;
+  const int64_t per_slot = 2LL * a.hk * kHead;
+  int cur = -1;  // ROPE: the row's new key, when this split holds it
+  uint4 k_cur = {}, v_cur = {};
+  if constexpr (ROPE) {
+    __shared__ float s_cos[kHead / 2], s_sin[kHead / 2];
+    const int p = a.pos[n];
+    if (threadIdx.x < kHead / 2) sincosf(qwen3_angle(p, threadIdx.x, a.theta), &s_sin[threadIdx.x], &s_cos[threadIdx.x]);
+    __syncthreads();
+    float cs[8], sn[8], w[8];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    widen8(ldg16(qp + g * kHead), q[g]);
+    for (int e = 0; e < 8; ++e) {
+      cs[e] = s_cos[8 * (c & 7) + e];
+      sn[e] = s_sin[8 * (c & 7) + e];
+    }
+    const bool lo = c < 8;
+    widen8(ldg16(a.q_norm + 8 * c), w);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) q[g][e] *= a.scale_log2;
+    for (int g = 0; g < G; ++g) {
+      float x[8], v[8], o[8];
+      widen8(ldg16(qp + g * kHead), x);
+      rms_norm_head(x, w, a.eps, v);
+      rotate_half(v, cs, sn, lo, o);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[g][e] = round_bf16(o[e]) * a.scale_log2;
+    }
+    if (t0 <= p && p < t1) {
+      cur = p;
+      const bf16_t* row = a.qkv + (int64_t)n * a.q_stride + c * 8;
+      float x[8], v[8], o[8];
+      widen8(ldg16(a.k_norm + 8 * c), w);
+      widen8(ldg16(row + (int64_t)(a.hq + kh) * kHead), x);
+      rms_norm_head(x, w, a.eps, v);
+      rotate_half(v, cs, sn, lo, o);
+      k_cur = pack8(o);
+      v_cur = ldg16(row + (int64_t)(a.hq + a.hk + kh) * kHead);
+      if (threadIdx.x < 16) {  // one DPP row writes the slot's K and V head kh
+        bf16_t* slot = a.kv_w + (int64_t)a.slots[n] * per_slot + c * 8;
+        *reinterpret_cast<uint4*>(slot + (int64_t)kh * kHead) = k_cur;
+        *reinterpret_cast<uint4*>(slot + (int64_t)(a.hk + kh) * kHead) = v_cur;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      widen8(ldg16(qp + g * kHead), q[g]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[g][e] *= a.scale_log2;
+    }
   }
 
   const int32_t* pg = SLOTS == kSlotsDense ? nullptr : a.pages + a.indptr[s];
   const int64_t dense_first = SLOTS == kSlotsDense ? (int64_t)(n / a.dense_per) * a.dense_span : 0;
-  const int64_t per_slot = 2LL * a.hk * kHead;
   const bf16_t* kb = a.kv + (int64_t)kh * kHead + c * 8;
   const bf16_t* vb = a.kv + (int64_t)(a.hk + kh) * kHead + c * 8;
 
@@ -174,6 +225,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
     for (int i = 0; i < 8; ++i) x.kr[i] = ldg16_stream(kb + off[i]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) x.vr[i] = ldg16_stream(vb + off[i]);
+  };
+  // ROPE: the row's new key from registers (cur is wave-uniform). It is the
+  // split's last key (t1 - 1), so the keys clamped past the split read its
+  // slot too; they are replaced as well (their p is 0, but 0 times a stale
+  // NaN or infinity in the slot would still reach the sum).
+  auto patch_tile = [&](KVTile& x, int tb) __attribute__((always_inline)) {
+    if constexpr (ROPE) {
+      if (cur >= 0 && tb + kTileKeys > cur) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (tb + 4 * i + r >= cur) {
+            x.kr[i] = k_cur;
+            x.vr[i] = v_cur;
+          }
+      }
+    }
   };
   auto compute_tile = [&](const KVTile& x, int tb) __attribute__((always_inline)) {
     float sc[G][8];
@@ -235,6 +302,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + kStride, i);
       }
+      patch_tile(ta, tb);
       compute_tile(ta, tb);
     }
   } else if (tb0 < t1) {
@@ -250,12 +318,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + 2 * kStride, i);
       __builtin_amdgcn_sched_barrier(0);  // keep the next tile's loads ahead of this tile's math
+      patch_tile(ta, tb);
       compute_tile(ta, tb);
       if (tb + kStride >= t1) break;
       load_tile(ta, tb + 2 * kStride, pid);
 #pragma unroll
       for (int i = 0; i < 8; ++i) pid[i] = page_of(tb + 3 * kStride, i);
       __builtin_amdgcn_sched_barrier(0);
+      patch_tile(tn, tb + kStride);
       compute_tile(tn, tb + kStride);
       if (tb + 2 * kStride >= t1) break;
     }
@@ -802,12 +872,13 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   if (a.fp8) return launch_decode_fp8(a, rows, stream);
   const int slots = a.len_mode == 2 ? kSlotsDense : a.pd.page % 4 == 0 ? kSlotsUniform : kSlotsLane;
   const bool div = !page_pow2(a.pd);
-#define OMNI_DECODE(K, G)                                                                              \
-  (slots == kSlotsDense   ? K<G, kSlotsDense, false><<<grid, kDecodeThreads, 0, stream>>>(a)           \
-   : div && slots == kSlotsUniform ? K<G, kSlotsUniform, true><<<grid, kDecodeThreads, 0, stream>>>(a) \
-   : div                           ? K<G, kSlotsLane, true><<<grid, kDecodeThreads, 0, stream>>>(a)    \
-   : slots == kSlotsUniform        ? K<G, kSlotsUniform, false><<<grid, kDecodeThreads, 0, stream>>>(a) \
-                                   : K<G, kSlotsLane, false><<<grid, kDecodeThreads, 0, stream>>>(a))
+#define OMNI_DECODE_R(K, G, R)                                                                                  \
+  (slots == kSlotsDense   ? K<G, kSlotsDense, false, false><<<grid, kDecodeThreads, 0, stream>>>(a)             \
+   : div && slots == kSlotsUniform ? K<G, kSlotsUniform, true, R><<<grid, kDecodeThreads, 0, stream>>>(a)       \
+   : div                           ? K<G, kSlotsLane, true, R><<<grid, kDecodeThreads, 0, stream>>>(a)          \
+   : slots == kSlotsUniform        ? K<G, kSlotsUniform, false, R><<<grid, kDecodeThreads, 0, stream>>>(a)      \
+                                   : K<G, kSlotsLane, false, R><<<grid, kDecodeThreads, 0, stream>>>(a))
+#define OMNI_DECODE(K, G) (a.rope ? OMNI_DECODE_R(K, G, true) : OMNI_DECODE_R(K, G, false))
   // Paged bf16 slots: H adjacent K/V heads per workgroup (the plan's
   // group_heads; 0 picks 2 for MHA when that still leaves >= 2048 workgroups,
   // else 1). Measured on the 128-session MHA tick: H = 2 505-508 us against
@@ -817,7 +888,8 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   // workgroup (a three-dimensional grid) when it would not.
   const int64_t mh_units = (int64_t)rows * a.hk * a.splits;
   int mh = 0;
-  if (slots != kSlotsDense)
+  if (a.rope && (slots == kSlotsDense || a.len_mode != 0 || a.ragged || a.group_heads > 1)) return -2;
+  if (slots != kSlotsDense && !a.rope)
     mh = a.group_heads > 0 ? a.group_heads
                            : (a.hq == a.hk && a.hk % 2 == 0 && mh_units / 2 >= 2048 && mh_units / 2 <= INT32_MAX ? 2 : 1);
   if (mh > 1 && mh_units / mh > INT32_MAX) return -2;
@@ -858,6 +930,7 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
     default: return -2;
   }
 #undef OMNI_DECODE
+#undef OMNI_DECODE_R
   if (check_launch() != 0) return -3;
   if (a.splits > 1) {
     decode_combine<<<dim3(a.hq, rows), 64, 0, stream>>>(a);

@@ -22,6 +22,7 @@
 // same slot of its registers, one row_ror:8 DPP move away.
 #include "common.h"
 #include "kernels.h"
+#include "rotary.h"
 
 #include <algorithm>
 
@@ -39,13 +40,6 @@ __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp<kRowMirror>(v));
   return v;
 }
-
-__device__ __forceinline__ uint4 pack8(const float* v) {
-  return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                    pack_bf16x2(v[6], v[7]));
-}
-
-__device__ __forceinline__ float round_bf16(float v) { return __uint_as_float(f2bf(v) << 16); }
 
 // Eight f32 to FP8 E4M3 (OCP, round to nearest even) on v_cvt_pk_fp8_f32.
 // Callers pass values already scaled into [-448, 448].
@@ -72,7 +66,7 @@ __device__ __forceinline__ void row_angles(const RopeArgs& a, int n, int p, floa
     } else {
       int pe = p;
       if constexpr (MODE == kMRope) pe = a.pos[3LL * n + (i < 3 * a.mrope_hw ? i % 3 : 0)];
-      ang = (float)pe * (1.f / powf(a.theta, (float)(2 * i) / kHead));
+      ang = qwen3_angle(pe, i, a.theta);
     }
     sincosf(ang, &s_sin[i], &s_cos[i]);
   }
@@ -124,20 +118,12 @@ __global__ __launch_bounds__(kRopeThreads) void norm_rope(RopeArgs a) {
     }
     float x[8];
     widen8(raw, x);
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
-    const float r = rsqrtf(row16_sum(ss) / kHead + a.eps);
     const bool is_q = head < a.hq;
-    float v[8];
+    float ws[8], v[8], o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = round_bf16(x[e] * r) * w[is_q ? 0 : 1][e];
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float partner = dpp<kRowRor8>(v[e]);  // element i + 64 for a low lane, i - 64 for a high one
-      o[e] = lo ? v[e] * cs[e] - partner * sn[e] : v[e] * cs[e] + partner * sn[e];
-    }
+    for (int e = 0; e < 8; ++e) ws[e] = is_q ? w[0][e] : w[1][e];
+    rms_norm_head(x, ws, a.eps, v);
+    rotate_half(v, cs, sn, lo, o);
     bf16_t* dst = is_q ? row + (int64_t)head * kHead
                        : (MODE == kMRope ? a.k_cache + (slot * a.hk + (head - a.hq)) * kHead
                                          : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead);

@@ -49,6 +49,7 @@ EXPORTS = (
     "omni_lm_dep_kv_attend",
     "omni_qwen3_rope",
     "omni_qwen3_rope_dense",
+    "omni_qwen3_rope_attend",
     "omni_lm_rope",
     "omni_hidream_qk_rope",
     "omni_attn_rows_new",
@@ -140,6 +141,7 @@ def load(path: str | None = None):
         "omni_lm_dep_kv_attend": [P, P, i32, P, i32, i32, f32, P],
         "omni_qwen3_rope": [P, P, P, P, P, P, i32, i32, i32, f32, f32, P],
         "omni_qwen3_rope_dense": [P, P, P, P, i32, i32, i32, i32, i32, i32, f32, f32, P],
+        "omni_qwen3_rope_attend": [P, P, P, P, P, P, P, P, i32, P, i32, i32, f32, f32, f32, dplan, P, P],
         "omni_lm_rope": [P, P, P, P, i32, i32, f32, P],
         "omni_hidream_qk_rope": [P, i32, P, P, P, P, P, P, i32, i32, i32, i32, f32, f32, P],
         "omni_attn_version": [],
@@ -380,6 +382,21 @@ def qwen3_rope(qkv, q_norm, k_norm, pos, slots, kv, rows, hq, hk, eps, theta, st
     _i32_dev(pos, "pos"), _i32_dev(slots, "slots")
     _check(load().omni_qwen3_rope(_ptr(qkv), _ptr(q_norm), _ptr(k_norm), _ptr(pos), _ptr(slots), _ptr(kv), rows, hq,
                                   hk, float(eps), float(theta), _stream(stream)))
+
+
+def qwen3_rope_attend(qkv, q_norm, k_norm, pos, slots, kv, indptr, pages, page, out, hq, hk, eps, theta, scale, plan,
+                      workspace=None, stream=None):
+    """``qwen3_rope`` then ``qwen3_attend`` (ragged = 0) in one launch: K and V
+    of row n written to ``slots[n]`` (which must be the slot of key pos[n]),
+    q rotated in registers only (qkv is not written)."""
+    for t, n in ((qkv, "qkv"), (q_norm, "q_norm"), (k_norm, "k_norm"), (kv, "kv"), (out, "out")):
+        _bf16_dev(t, n)
+    for t, n in ((pos, "pos"), (slots, "slots"), (indptr, "indptr"), (pages, "pages")):
+        _i32_dev(t, n)
+    _check(load().omni_qwen3_rope_attend(_ptr(qkv), _ptr(q_norm), _ptr(k_norm), _ptr(pos), _ptr(slots), _ptr(kv),
+                                         _ptr(indptr), _ptr(pages), page, _ptr(out), hq, hk, float(eps), float(theta),
+                                         float(scale), ctypes.byref(plan), _ws(plan, workspace), _stream(stream)))
+    return out
 
 
 def qwen3_rope_dense(qkv, q_norm, k_norm, kv, rows, per, base, span, hq, hk, eps, theta, stream=None):

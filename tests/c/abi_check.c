@@ -271,6 +271,24 @@ static void check_head64_validation(void) {
   CHECK(omni_mimi_rope_kv(kFake, kFake, kFake, kFake, 0, 2, 8, -0.28f, 250, 64000, NULL) == OMNI_ATTN_OK);
   CHECK(omni_lm_copy_kv(kFake, kFake, kFake, 3, 8440, NULL) == OMNI_ATTN_EINVAL);
   CHECK(omni_lm_copy_kv(NULL, NULL, NULL, 0, 8448, NULL) == OMNI_ATTN_OK);
+  {
+    omni_attn_decode_plan p;
+    CHECK(omni_attn_decode_plan_init(4, 16, 8, 16, 600, 256, &p) == OMNI_ATTN_OK);
+    /* bad eps; null slots; a head-group plan; a plan made for other heads */
+    CHECK(omni_qwen3_rope_attend(kFake, kFake, kFake, kFake, kFake, kFake, kFake, kFake, 16, kFake, 16, 8, -1.0f,
+                                 1e6f, 0.1f, &p, kFake, NULL) == OMNI_ATTN_EINVAL);
+    CHECK(omni_qwen3_rope_attend(kFake, kFake, kFake, kFake, NULL, kFake, kFake, kFake, 16, kFake, 16, 8, 1e-6f,
+                                 1e6f, 0.1f, &p, kFake, NULL) == OMNI_ATTN_EINVAL);
+    p.group_heads = 2;
+    CHECK(omni_qwen3_rope_attend(kFake, kFake, kFake, kFake, kFake, kFake, kFake, kFake, 16, kFake, 16, 8, 1e-6f,
+                                 1e6f, 0.1f, &p, kFake, NULL) == OMNI_ATTN_EINVAL);
+    p.group_heads = 0;
+    CHECK(omni_qwen3_rope_attend(kFake, kFake, kFake, kFake, kFake, kFake, kFake, kFake, 16, kFake, 32, 8, 1e-6f,
+                                 1e6f, 0.1f, &p, kFake, NULL) == OMNI_ATTN_EINVAL);
+    CHECK(omni_attn_decode_plan_init(0, 16, 8, 16, 600, 256, &p) == OMNI_ATTN_OK);
+    CHECK(omni_qwen3_rope_attend(NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 16, NULL, 16, 8, 1e-6f, 1e6f, 0.1f,
+                                 &p, NULL, NULL) == OMNI_ATTN_OK);
+  }
 }
 
 int main(void) {
