@@ -102,6 +102,16 @@ class DecodeBench:
         self.ws = oa.workspace_for(self.plan)
         self.bytes_per_layer = [W.fp8_kv_bytes(cs) if fp8 else cs.kv_bytes() for cs in self.cases]
         self.oa = oa
+        self.mode = "attend"
+        if cfg == 2:
+            # The step's rotary inputs: each row's new key goes to the slot the
+            # page table gives its position (what the engines' Rows builder makes).
+            for case, d in zip(self.cases, self.dev):
+                sl = [case.pages[case.indptr[n] + p // case.page] * case.page + p % case.page
+                      for n, p in enumerate(case.pos)]
+                d["slots"] = torch.from_numpy(np.asarray(sl, dtype=np.int32)).cuda()
+            self.q_norm = (1 + 0.1 * torch.randn(128, device="cuda", generator=gen)).to(torch.bfloat16)
+            self.k_norm = (1 + 0.1 * torch.randn(128, device="cuda", generator=gen)).to(torch.bfloat16)
 
     def layer(self, i, stream):
         d, c = self.dev[i], self.cases[i]
@@ -111,7 +121,14 @@ class DecodeBench:
         elif self.lm:
             self.oa.lm_attend(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page, d["out"],
                               c.hq, c.scale, c.context, self.plan, self.ws, stream)
+        elif self.mode == "fused":
+            self.oa.qwen3_rope_attend(d["qkv"], self.q_norm, self.k_norm, d["pos"], d["slots"], d["kv"], d["indptr"],
+                                      d["pages"], c.page, d["out"], c.hq, c.hk, 1e-6, 1e6, c.scale, self.plan, self.ws,
+                                      stream)
         else:
+            if self.mode == "rope_attend":
+                self.oa.qwen3_rope(d["qkv"], self.q_norm, self.k_norm, d["pos"], d["slots"], d["kv"], c.rows, c.hq,
+                                   c.hk, 1e-6, 1e6, stream)
             self.oa.qwen3_attend(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page,
                                  d["out"], c.hq, c.hk, c.scale, self.plan, self.ws, stream)
 
@@ -793,6 +810,26 @@ def main():
                                 graph_ms_per_step=round(g2, 4), graph_gbs=round(tb / (g2 * 1e-3) / 1e9, 1),
                                 graph_frac=round(tb / (g2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         log(f"[bench] {extra['config2']}")
+        # The whole per-layer step of the Qwen3-TTS talker's attention: rotary
+        # + K/V scatter then attention as two launches (the reference's
+        # sequence), against the fused launch.
+        step = {}
+        for mode in ("rope_attend", "fused"):
+            b2.mode = mode
+            ms, _ = time_steps(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream)
+            gms = float("nan") if args.no_graph else graph_step_ms(lambda s, e: b2.step(s, e), args.steps,
+                                                                   args.warmup, stream)
+            step[mode] = (ms, gms)
+        b2.mode = "attend"
+        extra["config2_step"] = dict(
+            workload="config2 per-layer step: qwen3_rope + qwen3_attend (two launches) against omni_qwen3_rope_attend",
+            separate_us_per_layer=round(step["rope_attend"][0] * 1e3 / b2.layers, 2),
+            fused_us_per_layer=round(step["fused"][0] * 1e3 / b2.layers, 2),
+            separate_graph_us_per_layer=round(step["rope_attend"][1] * 1e3 / b2.layers, 2),
+            fused_graph_us_per_layer=round(step["fused"][1] * 1e3 / b2.layers, 2),
+            attend_only_us_per_layer=round(ms2 * 1e3 / b2.layers, 2),
+            attend_only_graph_us_per_layer=round(g2 * 1e3 / b2.layers, 2))
+        log(f"[bench] {extra['config2_step']}")
         del b2
         torch.cuda.empty_cache()
     if args.only in (0, 6):

@@ -132,8 +132,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
   int cur = -1;  // ROPE: the row's new key, when this split holds it
   uint4 k_cur = {}, v_cur = {};
   if constexpr (ROPE) {
+    // Every load of the prologue (q, the norm weights, the new key's k and v
+    // rows) is issued before the angle table's math and barrier.
+    const int p = len - 1;  // pos[n]: decode rows see pos[n] + 1 keys
+    uint4 q_raw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) q_raw[g] = ldg16(qp + g * kHead);
+    const uint4 wq_raw = ldg16(a.q_norm + 8 * c);
+    uint4 wk_raw = {};
+    if (t0 <= p && p < t1) {
+      cur = p;
+      const bf16_t* row = a.qkv + (int64_t)n * a.q_stride + c * 8;
+      wk_raw = ldg16(a.k_norm + 8 * c);
+      k_cur = ldg16(row + (int64_t)(a.hq + kh) * kHead);
+      v_cur = ldg16(row + (int64_t)(a.hq + a.hk + kh) * kHead);
+    }
     __shared__ float s_cos[kHead / 2], s_sin[kHead / 2];
-    const int p = a.pos[n];
     if (threadIdx.x < kHead / 2) sincosf(qwen3_angle(p, threadIdx.x, a.theta), &s_sin[threadIdx.x], &s_cos[threadIdx.x]);
     __syncthreads();
     float cs[8], sn[8], w[8];
@@ -143,26 +157,23 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
       sn[e] = s_sin[8 * (c & 7) + e];
     }
     const bool lo = c < 8;
-    widen8(ldg16(a.q_norm + 8 * c), w);
+    widen8(wq_raw, w);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float x[8], v[8], o[8];
-      widen8(ldg16(qp + g * kHead), x);
+      widen8(q_raw[g], x);
       rms_norm_head(x, w, a.eps, v);
       rotate_half(v, cs, sn, lo, o);
 #pragma unroll
       for (int e = 0; e < 8; ++e) q[g][e] = round_bf16(o[e]) * a.scale_log2;
     }
-    if (t0 <= p && p < t1) {
-      cur = p;
-      const bf16_t* row = a.qkv + (int64_t)n * a.q_stride + c * 8;
+    if (cur >= 0) {
       float x[8], v[8], o[8];
-      widen8(ldg16(a.k_norm + 8 * c), w);
-      widen8(ldg16(row + (int64_t)(a.hq + kh) * kHead), x);
+      widen8(wk_raw, w);
+      widen8(k_cur, x);
       rms_norm_head(x, w, a.eps, v);
       rotate_half(v, cs, sn, lo, o);
       k_cur = pack8(o);
-      v_cur = ldg16(row + (int64_t)(a.hq + a.hk + kh) * kHead);
       if (threadIdx.x < 16) {  // one DPP row writes the slot's K and V head kh
         bf16_t* slot = a.kv_w + (int64_t)a.slots[n] * per_slot + c * 8;
         *reinterpret_cast<uint4*>(slot + (int64_t)kh * kHead) = k_cur;
