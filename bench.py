@@ -737,7 +737,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the HIP-graph replays (profiling runs: the trace then ends on the timed calls)")
-    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions)")
+    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions; 9 = config 2 rotary + attention step, separate and fused)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
     ap.add_argument("--build-peaks", action="store_true", help="compile bench_peaks.hip into bench_peaks.so and exit")
@@ -810,25 +810,28 @@ def main():
                                 graph_ms_per_step=round(g2, 4), graph_gbs=round(tb / (g2 * 1e-3) / 1e9, 1),
                                 graph_frac=round(tb / (g2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         log(f"[bench] {extra['config2']}")
+        del b2
+        torch.cuda.empty_cache()
+    if args.only in (0, 9):
         # The whole per-layer step of the Qwen3-TTS talker's attention: rotary
         # + K/V scatter then attention as two launches (the reference's
-        # sequence), against the fused launch.
+        # sequence), against the fused launch, and attention alone.
+        log("[bench] config 2 step: rotary + attention, separate and fused")
+        b2 = DecodeBench(2, args.pools, chunk=args.chunk)
         step = {}
-        for mode in ("rope_attend", "fused"):
+        for mode in ("attend", "rope_attend", "fused"):
             b2.mode = mode
             ms, _ = time_steps(lambda s, e: b2.step(s, e), args.steps, args.warmup, stream)
             gms = float("nan") if args.no_graph else graph_step_ms(lambda s, e: b2.step(s, e), args.steps,
                                                                    args.warmup, stream)
-            step[mode] = (ms, gms)
-        b2.mode = "attend"
+            step[mode] = (ms * 1e3 / b2.layers, gms * 1e3 / b2.layers)
         extra["config2_step"] = dict(
             workload="config2 per-layer step: qwen3_rope + qwen3_attend (two launches) against omni_qwen3_rope_attend",
-            separate_us_per_layer=round(step["rope_attend"][0] * 1e3 / b2.layers, 2),
-            fused_us_per_layer=round(step["fused"][0] * 1e3 / b2.layers, 2),
-            separate_graph_us_per_layer=round(step["rope_attend"][1] * 1e3 / b2.layers, 2),
-            fused_graph_us_per_layer=round(step["fused"][1] * 1e3 / b2.layers, 2),
-            attend_only_us_per_layer=round(ms2 * 1e3 / b2.layers, 2),
-            attend_only_graph_us_per_layer=round(g2 * 1e3 / b2.layers, 2))
+            separate_us_per_layer=round(step["rope_attend"][0], 2), fused_us_per_layer=round(step["fused"][0], 2),
+            attend_only_us_per_layer=round(step["attend"][0], 2),
+            separate_graph_us_per_layer=round(step["rope_attend"][1], 2),
+            fused_graph_us_per_layer=round(step["fused"][1], 2),
+            attend_only_graph_us_per_layer=round(step["attend"][1], 2))
         log(f"[bench] {extra['config2_step']}")
         del b2
         torch.cuda.empty_cache()
@@ -857,7 +860,7 @@ def main():
         extra["short"] = short_bench(stream, args.steps, args.warmup)
         log(f"[bench] {extra['short']}")
         torch.cuda.empty_cache()
-    if args.only in (4, 5, 2, 6, 7, 8):
+    if args.only in (4, 5, 2, 6, 7, 8, 9):
         print(json.dumps({"extra": extra}), flush=True)
         return
 
