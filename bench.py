@@ -831,7 +831,10 @@ def main():
             attend_only_us_per_layer=round(step["attend"][0], 2),
             separate_graph_us_per_layer=round(step["rope_attend"][1], 2),
             fused_graph_us_per_layer=round(step["fused"][1], 2),
-            attend_only_graph_us_per_layer=round(step["attend"][1], 2))
+            attend_only_graph_us_per_layer=round(step["attend"][1], 2),
+            # attention alone timed per step (no events between calls), as a fraction of 8 TB/s
+            attend_only_frac=round(sum(b2.bytes_per_layer) / b2.layers / (step["attend"][0] * 1e-6) / 1e9
+                                   / HBM_PEAK_GBS, 4))
         log(f"[bench] {extra['config2_step']}")
         del b2
         torch.cuda.empty_cache()
