@@ -262,7 +262,8 @@ int omni_qwen3_rope(void* qkv, const void* q_norm, const void* k_norm, const int
  * n is taken from the rotated row, so slots[n] must be the slot the page
  * table gives key pos[n] (what the engines' Rows builder produces), and no
  * other row of the call may read slots[n]. The plan is a decode plan
- * (group_heads 0 or 1). */
+ * (group_heads 0 or 1: the fused kernel runs one K/V head per workgroup, so
+ * for MHA it matches omni_qwen3_attend with group_heads = 1 bit for bit). */
 int omni_qwen3_rope_attend(const void* qkv, const void* q_norm, const void* k_norm, const int32_t* pos,
                            const int32_t* slots, void* kv, const int32_t* indptr, const int32_t* pages, int page,
                            void* out, int hq, int hk, float eps, float theta, float scale,

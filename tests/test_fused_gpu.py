@@ -6,7 +6,9 @@ from registers where the separate path reads back what qwen3_rope wrote),
 and qkv is left as it was. The chain is also held to the oracle's chain
 (oracle qwen3_rope, then oracle paged attention) at config 2's full size.
 The new key's slot is filled with NaN before each call, so a kernel that
-read it instead of the registers would not return finite values."""
+read it instead of the registers would not return finite values. For MHA
+both paths run one K/V head per workgroup (the separate call could pick two,
+a different summation order)."""
 import numpy as np
 import pytest
 import torch
@@ -39,6 +41,9 @@ def run_both(c, chunk=0, seed=0):
     kv0 = c.kv.copy()
     kv0.reshape(kv0.shape[0], -1)[slots] = 0x7FC0  # NaN where the new keys go
     plan = oa.decode_plan(c.rows, hq, hk, c.page, int(c.pos.max()) + 1, chunk)
+    # The fused kernel takes one K/V head per workgroup; for MHA the separate
+    # call may otherwise pick two (a different summation order), so both run one.
+    plan.group_heads = 1 if hq == hk else 0
     ws = oa.workspace_for(plan)
     pos, sl, seq = dev_i32(c.pos), dev_i32(slots), dev_i32(c.seq)
     indptr, pages = dev_i32(c.indptr), dev_i32(c.pages)
@@ -159,3 +164,22 @@ def test_fused_step_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(got_out.view(torch.int16), out.view(torch.int16)), f"replay {rep}: output"
         assert torch.equal(got_kv.view(torch.int16), kv.view(torch.int16)), f"replay {rep}: K/V"
+
+
+PAGES = [1, 2, 3, 4, 8, 12, 16, 20, 24, 32, 48, 64]
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_fused_sweep(case):
+    """Seeded random shapes: GQA ratio, page size (powers of two and not),
+    rows, lengths and split size drawn per case; fused = separate bit for bit."""
+    rng = np.random.default_rng(3000 + case)
+    hq, hk = [(16, 8), (32, 8), (8, 8), (32, 32), (16, 4), (8, 2)][rng.integers(0, 6)]
+    page = int(rng.choice(PAGES))
+    rows = int(rng.integers(1, 49))
+    lo = int(rng.integers(1, 600))
+    hi = lo + int(rng.integers(0, 1200))
+    chunk = int(rng.choice([0, 128, 256, 512]))
+    c = W.paged_decode_case(rows, hq, hk, lo, hi, page=page, seed=case, slack_pages=3)
+    check_identical(c, chunk=chunk, seed=case,
+                    what=f"fused case {case}: {hq}/{hk} page {page} rows {rows} len [{lo}, {hi}] chunk {chunk}")
