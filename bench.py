@@ -103,6 +103,15 @@ class DecodeBench:
         self.bytes_per_layer = [W.fp8_kv_bytes(cs) if fp8 else cs.kv_bytes() for cs in self.cases]
         self.oa = oa
         self.mode = "attend"
+        if fp8:
+            # lm_rope's slot for each row: the lease's slot of ring index pos % context.
+            for case, d in zip(self.cases, self.dev):
+                sl = []
+                for n, p in enumerate(case.pos):
+                    t = int(p) % case.context
+                    sl.append(case.pages[case.indptr[n] + t // case.page] * case.page + t % case.page)
+                d["slots"] = torch.from_numpy(np.asarray(sl, dtype=np.int32)).cuda()
+            self.coef = float(np.float32(-np.log(10000.0) * 2.0 / 128))
         if cfg == 2:
             # The step's rotary inputs: each row's new key goes to the slot the
             # page table gives its position (what the engines' Rows builder makes).
@@ -115,7 +124,12 @@ class DecodeBench:
 
     def layer(self, i, stream):
         d, c = self.dev[i], self.cases[i]
-        if self.fp8:
+        if self.fp8 and self.mode == "fused":
+            self.oa.lm_rope_attend_fp8(d["qkv"], d["pos"], d["slots"], d["kv"], d["indptr"], d["pages"], c.page,
+                                       d["out"], c.hq, self.coef, c.scale, c.context, self.plan, self.ws, stream)
+        elif self.fp8:
+            if self.mode == "rope_attend":
+                self.oa.lm_rope(d["qkv"], d["pos"], d["slots"], d["kv"], c.rows, c.hq, self.coef, stream)
             self.oa.lm_attend_fp8(d["qkv"], d["kv"], d["pos"], d["seq"], 0, d["indptr"], d["pages"], c.page,
                                   d["out"], c.hq, c.scale, c.context, self.plan, self.ws, stream)
         elif self.lm:
@@ -737,7 +751,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="skip the HIP-graph replays (profiling runs: the trace then ends on the timed calls)")
-    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions; 9 = config 2 rotary + attention step, separate and fused)")
+    ap.add_argument("--only", type=int, default=0, help="time only this config (2, 3, 4 or 5; 6 = config 3 over FP8 slots; 7 = rotary + scatter; 8 = dense and head-64 attentions; 9 = the rotary + attention steps of config 2 and config 3 over FP8 slots, separate and fused)")
     ap.add_argument("--calib-copy-mib", type=int, default=0, help="run the copy calibration kernel and exit")
     ap.add_argument("--peaks", action="store_true", help="print the measured peaks and exit")
     ap.add_argument("--build-peaks", action="store_true", help="compile bench_peaks.hip into bench_peaks.so and exit")
@@ -837,6 +851,28 @@ def main():
                                    / HBM_PEAK_GBS, 4))
         log(f"[bench] {extra['config2_step']}")
         del b2
+        torch.cuda.empty_cache()
+        # The same for PersonaPlex's tick over its FP8 cache: lm_rope then
+        # lm_attend (two launches) against the fused launch.
+        log("[bench] config 3 FP8 step: rotary + quantized scatter + attention, separate and fused")
+        b8 = DecodeBench(3, args.pools, chunk=args.chunk, fp8=True)
+        step = {}
+        for mode in ("attend", "rope_attend", "fused"):
+            b8.mode = mode
+            ms, _ = time_steps(lambda s, e: b8.step(s, e), args.steps, args.warmup, stream)
+            gms = float("nan") if args.no_graph else graph_step_ms(lambda s, e: b8.step(s, e), args.steps,
+                                                                   args.warmup, stream)
+            step[mode] = (ms * 1e3 / b8.layers, gms * 1e3 / b8.layers)
+        extra["config3_fp8_step"] = dict(
+            workload="config3 over FP8 slots, per-layer step: lm_rope + lm_attend (two launches) against "
+                     "omni_lm_rope_attend_fp8",
+            separate_us_per_layer=round(step["rope_attend"][0], 2), fused_us_per_layer=round(step["fused"][0], 2),
+            attend_only_us_per_layer=round(step["attend"][0], 2),
+            separate_graph_us_per_layer=round(step["rope_attend"][1], 2),
+            fused_graph_us_per_layer=round(step["fused"][1], 2),
+            attend_only_graph_us_per_layer=round(step["attend"][1], 2))
+        log(f"[bench] {extra['config3_fp8_step']}")
+        del b8
         torch.cuda.empty_cache()
     if args.only in (0, 6):
         log("[bench] config 3 decode over FP8 E4M3 slots")

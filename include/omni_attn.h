@@ -283,6 +283,21 @@ int omni_qwen3_rope_dense(void* qkv, const void* q_norm, const void* k_norm, voi
 int omni_lm_rope(void* qkv, const int32_t* pos, const int32_t* slots, void* kv, int rows, int heads, float coef,
                  void* stream);
 
+/* omni_lm_rope followed by omni_lm_attend_fp8 on decode rows (ragged = 0: row n
+ * is sequence n and attends to min(pos[n] + 1, context) ring slots), in one
+ * launch; it has no counterpart in the reference, which runs the two as
+ * separate launches (crates/omni-personaplex/src/helium.rs:242-275). The
+ * output and the FP8 bytes and scales written to slot slots[n] are
+ * bit-identical to the two calls'. Differences: q is rotated in registers only
+ * (qkv is not written), and ring index pos[n] % context of row n is taken from
+ * the rotated, quantized row, so slots[n] must be the slot the page table gives
+ * that ring index (what the engines' Rows builder produces), and no other row
+ * of the call may read slots[n]. The plan is the FP8 decode plan (hq = hk =
+ * heads; its group_heads may fix the heads per workgroup). */
+int omni_lm_rope_attend_fp8(const void* qkv, const int32_t* pos, const int32_t* slots, void* kv, const int32_t* indptr,
+                            const int32_t* pages, int page, void* out, int heads, float coef, float scale, int context,
+                            const omni_attn_decode_plan* plan, void* workspace, void* stream);
+
 /* Replaces `hidream_qk_rope` (crates/omni-hidream-o1/kernels/hidream.cu:55-106):
  * RMSNorm as qwen3_rope, then Qwen3-VL's interleaved M-RoPE: row n has
  * positions (t, h, w) at positions[3n..3n+2]; pair i turns by the h position

@@ -125,6 +125,7 @@ int decode_common(const void* qkv, const void* kv, const int32_t* pos, const int
     a.kv_w = rope->kv_w;
     a.eps = rope->eps;
     a.theta = rope->theta;
+    a.coef = rope->coef;
   }
   const int rc = omni::launch_decode(a, plan->rows, as_stream(stream));
   if (rc == -2)
@@ -654,6 +655,22 @@ int omni_qwen3_rope_attend(const void* qkv, const void* q_norm, const void* k_no
   r.theta = theta;
   return decode_common(qkv, kv, pos, nullptr, 0, indptr, pages, page, out, hq, hk, scale, 0, 0, plan, workspace,
                        stream, 0, 0, 0, 0, &r);
+}
+
+int omni_lm_rope_attend_fp8(const void* qkv, const int32_t* pos, const int32_t* slots, void* kv, const int32_t* indptr,
+                            const int32_t* pages, int page, void* out, int heads, float coef, float scale, int context,
+                            const omni_attn_decode_plan* plan, void* workspace, void* stream) {
+  if (context <= 0) return fail(OMNI_ATTN_EINVAL, "lm_rope_attend_fp8: context=%d", context);
+  if (plan && plan->rows > 0) {
+    if (!slots) return fail(OMNI_ATTN_EINVAL, "lm_rope_attend_fp8: null slots");
+    if (!std::isfinite(coef)) return fail(OMNI_ATTN_EINVAL, "lm_rope_attend_fp8: non-finite coef");
+  }
+  omni::DecodeArgs r{};
+  r.slots = slots;
+  r.kv_w = static_cast<omni::bf16_t*>(kv);
+  r.coef = coef;
+  return decode_common(qkv, kv, pos, nullptr, 0, indptr, pages, page, out, heads, heads, scale, context, 0, plan,
+                       workspace, stream, 1, 0, 0, 0, &r);
 }
 
 int omni_qwen3_attend_dense(const void* qkv, const void* kv, int per, int base, int span, void* out, int hq, int hk,

@@ -174,11 +174,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
       rms_norm_head(x, w, a.eps, v);
       rotate_half(v, cs, sn, lo, o);
       k_cur = pack8(o);
-      if (threadIdx.x < 16) {  // one DPP row writes the slot's K and V head kh
-        bf16_t* slot = a.kv_w + (int64_t)a.slots[n] * per_slot + c * 8;
-        *reinterpret_cast<uint4*>(slot + (int64_t)kh * kHead) = k_cur;
-        *reinterpret_cast<uint4*>(slot + (int64_t)(a.hk + kh) * kHead) = v_cur;
-      }
     }
   } else {
 #pragma unroll
@@ -340,6 +335,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split(DecodeArgs a) {
       compute_tile(tn, tb + kStride);
       if (tb + 2 * kStride >= t1) break;
     }
+  }
+
+  // ROPE: the new key's slot is written after the key loop (a store counts in
+  // vmcnt: issued before the loop, the first tile's wait would wait for it).
+  if (ROPE && cur >= 0 && threadIdx.x < 16) {  // one DPP row writes the slot's K and V head kh
+    bf16_t* slot = a.kv_w + (int64_t)a.slots[n] * per_slot + c * 8;
+    *reinterpret_cast<uint4*>(slot + (int64_t)kh * kHead) = k_cur;
+    *reinterpret_cast<uint4*>(slot + (int64_t)(a.hk + kh) * kHead) = v_cur;
   }
 
   // Rows of the wave hold disjoint keys under one shared max: add them up.
@@ -625,7 +628,13 @@ __device__ __forceinline__ float across_key_rows(float v) {
 // NI load instructions (NI * R keys) per wave and iteration. UP: the R keys of
 // one instruction share a page (page a multiple of R), so its id is a scalar
 // load.
-template <int H, int NI, bool UP, bool DIV>
+// ROPE: lm_rope fused in (omni_lm_rope_attend_fp8), decode rows only. Every
+// workgroup of row n turns its q heads as lm_rope does (rounded to bf16) from
+// the row's angle table in LDS. The split holding ring index pos[n] % context
+// (the row's new key) also turns k, quantizes K and V to E4M3 with their
+// per-head scales exactly as lm_rope does, writes them into slot slots[n],
+// and takes that key (and any key clamped onto it) from registers.
+template <int H, int NI, bool UP, bool DIV, bool ROPE>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a, int rows) {
   constexpr int R = 8 / H;
   // Workgroup i runs on XCD i % 8: the head groups of one (row, split) unit
@@ -650,12 +659,31 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
   const int kh = kg * H + hl;
 
   float q[16];
+  int cur = -1;  // ROPE: the row's new key, when this split holds it
+  uint4 kq_cur = {}, vq_cur = {};
+  float ks_cur = 0.f, vs_cur = 0.f;
+  [[maybe_unused]] int p_rope = 0;
+  [[maybe_unused]] uint4 q0r = {}, q1r = {}, k0r = {}, k1r = {}, v0r = {}, v1r = {};
   {
     const bf16_t* qp = a.qkv + (int64_t)n * a.q_stride + (int64_t)kh * kHead + c * 16;
-    widen8(ldg16(qp), q);
-    widen8(ldg16(qp + 8), q + 8);
+    if constexpr (ROPE) {
+      // The prologue's loads go out here; its math runs after the first
+      // tile's K/V loads are issued too (rope_prologue below).
+      p_rope = a.pos[n];
+      const int ring = p_rope % a.context;  // lm_rope writes slot(p % context)
+      // Loaded on every path (only the split holding the new key uses k and
+      // v), so the wait counts before the rotary math are the same on all paths.
+      q0r = ldg16(qp), q1r = ldg16(qp + 8);
+      const bf16_t* kp = a.qkv + (int64_t)n * a.q_stride + (int64_t)(a.hk + kh) * kHead + c * 16;
+      const bf16_t* vp = kp + (int64_t)a.hk * kHead;
+      k0r = ldg16(kp), k1r = ldg16(kp + 8), v0r = ldg16(vp), v1r = ldg16(vp + 8);
+      if (t0 <= ring && ring < t1) cur = ring;
+    } else {
+      widen8(ldg16(qp), q);
+      widen8(ldg16(qp + 8), q + 8);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) q[e] *= a.scale_log2;
+      for (int e = 0; e < 16; ++e) q[e] *= a.scale_log2;
+    }
   }
 
   const int32_t* pg = a.pages + a.indptr[s];
@@ -696,6 +724,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
       x.vs[i] = *reinterpret_cast<const float*>(sp + vsoff);
     }
   };
+  // ROPE: the row's new key from registers, for the lanes whose key (after
+  // clamping to the split) is it (cur is wave-uniform).
+  auto patch_tile = [&](Tile& x, int tb) {
+    if constexpr (ROPE) {
+      if (cur >= tb && (cur < tb + kKeys || cur == t1 - 1)) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+          if (min(tb + R * i + r, t1 - 1) == cur) {
+            x.kr[i] = kq_cur;
+            x.vr[i] = vq_cur;
+            x.ks[i] = ks_cur;
+            x.vs[i] = vs_cur;
+          }
+      }
+    }
+  };
   auto compute_tile = [&](const Tile& x, int tb) {
     float sc[NI];
 #pragma unroll
@@ -734,31 +778,106 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_fp8(DecodeArgs a,
     }
   };
   constexpr int kStride = kDecodeWaves * kKeys;
+  // ROPE: the rotary math (all waves: the angle table needs a barrier).
+  auto rope_prologue = [&]() {
+    __shared__ float s_cos[kHead / 2], s_sin[kHead / 2];
+    if (threadIdx.x < kHead / 2)
+      sincosf(expf((float)threadIdx.x * a.coef) * (float)p_rope, &s_sin[threadIdx.x], &s_cos[threadIdx.x]);
+    __syncthreads();
+    // Lane c holds pairs 8c .. 8c + 7 (elements 16c .. 16c + 15).
+    float cs[8], sn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      cs[j] = s_cos[8 * c + j];
+      sn[j] = s_sin[8 * c + j];
+    }
+    widen8(q0r, q);
+    widen8(q1r, q + 8);
+    rotate_interleaved<8>(q, cs, sn);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) q[e] = round_bf16(q[e]) * a.scale_log2;
+    if (cur >= 0) {
+      // K rotated (unrounded) and V as read, each quantized with its head's
+      // scale: the head's 128 values sit on 8 lanes, so its absmax is an
+      // 8-lane max (exact in any order).
+      float kx[16], vx[16];
+      widen8(k0r, kx);
+      widen8(k1r, kx + 8);
+      widen8(v0r, vx);
+      widen8(v1r, vx + 8);
+      rotate_interleaved<8>(kx, cs, sn);
+      float ka = 0.f, va = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        ka = fmaxf(ka, fabsf(kx[e]));
+        va = fmaxf(va, fabsf(vx[e]));
+      }
+      ka = fmaxf(ka, dpp<kQuadSwap1>(ka));
+      ka = fmaxf(ka, dpp<kQuadSwap2>(ka));
+      ka = fmaxf(ka, dpp<kRowHalfMirror>(ka));
+      va = fmaxf(va, dpp<kQuadSwap1>(va));
+      va = fmaxf(va, dpp<kQuadSwap2>(va));
+      va = fmaxf(va, dpp<kRowHalfMirror>(va));
+      ks_cur = e4m3_scale(ka);
+      vs_cur = e4m3_scale(va);
+      const float kinv = 1.f / ks_cur, vinv = 1.f / vs_cur;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        kx[e] *= kinv;
+        vx[e] *= vinv;
+      }
+      const uint2 klo = e4m3x8(kx), khi = e4m3x8(kx + 8), vlo = e4m3x8(vx), vhi = e4m3x8(vx + 8);
+      kq_cur = make_uint4(klo.x, klo.y, khi.x, khi.y);
+      vq_cur = make_uint4(vlo.x, vlo.y, vhi.x, vhi.y);
+    }
+  };
   const int tb0 = t0 + wave * kKeys;
-  if (tb0 < t1) {
-    int pid[NI];
-    Tile ta, tb_;
+  int pid[NI];
+  Tile ta, tb_;
+  // ROPE: on every wave, even one with no tile (its keys clamp to the split's
+  // last, a valid slot). A load issued on one path only would make the
+  // compiler's wait counts in the prologue assume it is the newest, and the
+  // prologue would wait for this whole tile before the loop issues the next.
+  if (ROPE || tb0 < t1) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0, i);
     load_tile(ta, tb0, pid);
 #pragma unroll
     for (int i = 0; i < NI; ++i) pid[i] = page_of(tb0 + kStride, i);
+  }
+  if constexpr (ROPE) rope_prologue();  // every wave: it holds a barrier
+  if (tb0 < t1) {
     for (int tb = tb0;; tb += 2 * kStride) {
       load_tile(tb_, tb + kStride, pid);
 #pragma unroll
       for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + 2 * kStride, i);
       __builtin_amdgcn_sched_barrier(0);  // keep the next tile's loads ahead of this tile's math
+      patch_tile(ta, tb);
       compute_tile(ta, tb);
       if (tb + kStride >= t1) break;
       load_tile(ta, tb + 2 * kStride, pid);
 #pragma unroll
       for (int i = 0; i < NI; ++i) pid[i] = page_of(tb + 3 * kStride, i);
       __builtin_amdgcn_sched_barrier(0);
+      patch_tile(tb_, tb + kStride);
       compute_tile(tb_, tb + kStride);
       if (tb + 2 * kStride >= t1) break;
     }
   }
 
+  // ROPE: the new key's slot is written after the key loop. A store counts
+  // in vmcnt, so one issued before the loop would make the first tile's wait
+  // wait for its acknowledgement too.
+  if (ROPE && cur >= 0 && threadIdx.x < 8 * H) {  // wave 0's key-row-0 lanes: heads kg H ..
+    uint8_t* slot = reinterpret_cast<uint8_t*>(a.kv_w) + (int64_t)a.slots[n] * a.slot_bytes;
+    *reinterpret_cast<uint4*>(slot + (int64_t)kh * kHead + c * 16) = kq_cur;
+    *reinterpret_cast<uint4*>(slot + (int64_t)(a.hk + kh) * kHead + c * 16) = vq_cur;
+    if (c == 0) {
+      float* scales = reinterpret_cast<float*>(slot + 2LL * a.hk * kHead);
+      scales[kh] = ks_cur;
+      scales[a.hk + kh] = vs_cur;
+    }
+  }
   // The key rows of the wave hold disjoint keys under one shared max.
   l = across_key_rows<H, false>(l);
 #pragma unroll
@@ -841,26 +960,35 @@ static int fp8_heads_per_group(const DecodeArgs& a, int rows) {
 // slots 280.8-280.9 against 282.7-283.1 us per call (one box, alternating).
 constexpr int kFp8OccupancyLds = 64 << 10;
 
-template <int H>
-static void launch_fp8_h(const DecodeArgs& a, int rows, hipStream_t stream) {
+template <int H, bool ROPE>
+static void launch_fp8_hr(const DecodeArgs& a, int rows, hipStream_t stream) {
   const int units = rows * a.splits;
   const dim3 grid(8 * (a.hk / H) * ((units + 7) / 8));
   constexpr int R = 8 / H;
   const bool up = a.pd.page % R == 0;
   if (!page_pow2(a.pd)) {
     if (up)
-      decode_split_fp8<H, 4, true, true><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
+      decode_split_fp8<H, 4, true, true, ROPE><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
     else
-      decode_split_fp8<H, 4, false, true><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
+      decode_split_fp8<H, 4, false, true, ROPE><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
   } else if (up) {
-    decode_split_fp8<H, 4, true, false><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
+    decode_split_fp8<H, 4, true, false, ROPE><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
   } else {
-    decode_split_fp8<H, 4, false, false><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
+    decode_split_fp8<H, 4, false, false, ROPE><<<grid, kDecodeThreads, kFp8OccupancyLds, stream>>>(a, rows);
   }
+}
+
+template <int H>
+static void launch_fp8_h(const DecodeArgs& a, int rows, hipStream_t stream) {
+  if (a.rope)
+    launch_fp8_hr<H, true>(a, rows, stream);
+  else
+    launch_fp8_hr<H, false>(a, rows, stream);
 }
 
 static int launch_decode_fp8(const DecodeArgs& a, int rows, hipStream_t stream) {
   if (a.hq != a.hk) return -2;
+  if (a.rope && (a.len_mode != 0 || a.ragged || a.context <= 0 || a.context == INT32_MAX)) return -2;
   // The one-dimensional grid (at most hk (rows splits + 7) workgroups) must fit an int.
   if ((int64_t)a.hk * ((int64_t)rows * a.splits + 7) > INT32_MAX) return -2;
   switch (fp8_heads_per_group(a, rows)) {

@@ -39,16 +39,17 @@ struct DecodeArgs {
   int64_t slot_bytes;  // bytes per FP8 slot: 2 hk 128 + 2 hk 4
   int group_heads;     // K/V heads per workgroup of the head-group kernels (0 = pick from the shape)
   int dense_per, dense_base, dense_span;  // dense rows (len_mode 2): slot (n / per) * span + t
-  // Fused Qwen3 rotary (rope != 0, decode rows only): q and the row's own key
-  // are normalised and rotated in the kernel, and the split holding key pos[n]
-  // writes the row's K and V into slot slots[n] of kv_w (the cache kv points
-  // to) and takes that key from registers.
+  // Fused rotary (rope != 0, decode rows only): q and the row's own key are
+  // rotated in the kernel (Qwen3: normalised first; FP8 ring: K and V
+  // quantized), and the split holding the row's new key writes it into slot
+  // slots[n] of kv_w (the cache kv points to) and takes it from registers.
   int rope;
   const bf16_t* q_norm;
   const bf16_t* k_norm;
   const int32_t* slots;
   bf16_t* kv_w;
   float eps, theta;
+  float coef;  // FP8 ring (lm_rope): pair i turns by p * exp(i * coef)
 };
 
 int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream);

@@ -41,16 +41,6 @@ __device__ __forceinline__ float row16_max(float v) {
   return v;
 }
 
-// Eight f32 to FP8 E4M3 (OCP, round to nearest even) on v_cvt_pk_fp8_f32.
-// Callers pass values already scaled into [-448, 448].
-__device__ __forceinline__ uint2 e4m3x8(const float* v) {
-  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
-  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], 0, false);
-  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
-  return make_uint2((uint32_t)lo, (uint32_t)hi);
-}
-
 constexpr int kPaged = 0, kDense = 1, kMRope = 2, kLm = 3;
 
 // The row's 64 rotary angles, cos and sin, into LDS: thread i < 64 takes pair
@@ -152,12 +142,7 @@ __global__ __launch_bounds__(kRopeThreads) void lm_rope_fp8(RopeArgs a) {
     float x[8];
     widen8(ldg16(row + (int64_t)head * kHead + 8 * c), x);
     if (head < 2 * heads) {  // q or k: rotate
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float re = x[2 * j], im = x[2 * j + 1];
-        x[2 * j] = re * cs[j] - im * sn[j];
-        x[2 * j + 1] = re * sn[j] + im * cs[j];
-      }
+      rotate_interleaved<4>(x, cs, sn);
       if (head < heads) {
         *reinterpret_cast<uint4*>(row + (int64_t)head * kHead + 8 * c) = pack8(x);
         continue;
@@ -169,7 +154,7 @@ __global__ __launch_bounds__(kRopeThreads) void lm_rope_fp8(RopeArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
     amax = row16_max(amax);
-    const float sc = fmaxf(amax * (1.f / 448.f), 1e-12f);
+    const float sc = e4m3_scale(amax);
     const float inv = 1.f / sc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] *= inv;

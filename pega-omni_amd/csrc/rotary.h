@@ -1,7 +1,7 @@
-// Qwen3 rotary helpers shared by the rotary + scatter kernel (rope.hip) and
-// the fused rotary + decode attention (decode.hip), so that both produce the
-// same bits for the same row. A head is held by one 16-lane DPP row, lane c
-// holding elements 8c .. 8c + 7.
+// Rotary and cache-write helpers shared by the rotary + scatter kernels
+// (rope.hip) and the fused rotary + decode attention (decode.hip), so that
+// both produce the same bits for the same row. Qwen3: a head is held by one
+// 16-lane DPP row, lane c holding elements 8c .. 8c + 7.
 #pragma once
 #include "common.h"
 
@@ -35,11 +35,42 @@ __device__ __forceinline__ void rms_norm_head(const float* x, const float* w, fl
 // in the same register slot (one row_ror:8 DPP move). lo: lane c < 8. cs, sn:
 // cos and sin of pairs 8 (c & 7) .. + 7.
 __device__ __forceinline__ void rotate_half(const float* v, const float* cs, const float* sn, bool lo, float* o) {
+  // No FMA contraction: whether a*b - c*d fuses, and which product, would
+  // otherwise depend on the caller's surrounding code, and callers must agree.
+#pragma clang fp contract(off)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float partner = dpp<kRowRor8>(v[e]);  // element i + 64 for a low lane, i - 64 for a high one
     o[e] = lo ? v[e] * cs[e] - partner * sn[e] : v[e] * cs[e] + partner * sn[e];
   }
+}
+
+// PersonaPlex's interleaved rotary (crates/omni-personaplex/kernels/lm.cu:
+// 125-182): pair j of x (elements 2j, 2j + 1) turns by the angle whose cos and
+// sin are cs[j], sn[j]; PAIRS pairs, in f32.
+template <int PAIRS>
+__device__ __forceinline__ void rotate_interleaved(float* x, const float* cs, const float* sn) {
+#pragma clang fp contract(off)  // as in rotate_half
+#pragma unroll
+  for (int j = 0; j < PAIRS; ++j) {
+    const float re = x[2 * j], im = x[2 * j + 1];
+    x[2 * j] = re * cs[j] - im * sn[j];
+    x[2 * j + 1] = re * sn[j] + im * cs[j];
+  }
+}
+
+// The FP8 E4M3 scale of a head whose largest magnitude is amax:
+// max(amax / 448, 1e-12); the values are stored as x * (1 / scale).
+__device__ __forceinline__ float e4m3_scale(float amax) { return fmaxf(amax * (1.f / 448.f), 1e-12f); }
+
+// Eight f32 to FP8 E4M3 (OCP, round to nearest even) on v_cvt_pk_fp8_f32.
+// Callers pass values already scaled into [-448, 448].
+__device__ __forceinline__ uint2 e4m3x8(const float* v) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
+  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], 0, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
+  return make_uint2((uint32_t)lo, (uint32_t)hi);
 }
 
 }  // namespace omni

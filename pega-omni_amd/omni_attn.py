@@ -50,6 +50,7 @@ EXPORTS = (
     "omni_qwen3_rope",
     "omni_qwen3_rope_dense",
     "omni_qwen3_rope_attend",
+    "omni_lm_rope_attend_fp8",
     "omni_lm_rope",
     "omni_hidream_qk_rope",
     "omni_attn_rows_new",
@@ -142,6 +143,7 @@ def load(path: str | None = None):
         "omni_qwen3_rope": [P, P, P, P, P, P, i32, i32, i32, f32, f32, P],
         "omni_qwen3_rope_dense": [P, P, P, P, i32, i32, i32, i32, i32, i32, f32, f32, P],
         "omni_qwen3_rope_attend": [P, P, P, P, P, P, P, P, i32, P, i32, i32, f32, f32, f32, dplan, P, P],
+        "omni_lm_rope_attend_fp8": [P, P, P, P, P, P, i32, P, i32, f32, f32, i32, dplan, P, P],
         "omni_lm_rope": [P, P, P, P, i32, i32, f32, P],
         "omni_hidream_qk_rope": [P, i32, P, P, P, P, P, P, i32, i32, i32, i32, f32, f32, P],
         "omni_attn_version": [],
@@ -396,6 +398,24 @@ def qwen3_rope_attend(qkv, q_norm, k_norm, pos, slots, kv, indptr, pages, page, 
     _check(load().omni_qwen3_rope_attend(_ptr(qkv), _ptr(q_norm), _ptr(k_norm), _ptr(pos), _ptr(slots), _ptr(kv),
                                          _ptr(indptr), _ptr(pages), page, _ptr(out), hq, hk, float(eps), float(theta),
                                          float(scale), ctypes.byref(plan), _ws(plan, workspace), _stream(stream)))
+    return out
+
+
+def lm_rope_attend_fp8(qkv, pos, slots, kv, indptr, pages, page, out, heads, coef, scale, context, plan,
+                       workspace=None, stream=None):
+    """``lm_rope`` then ``lm_attend`` over FP8 slots (ragged = 0) in one launch:
+    K and V of row n quantized into ``slots[n]`` (which must be the slot of ring
+    index pos[n] % context), q rotated in registers only (qkv is not written)."""
+    import torch
+    for t, n in ((qkv, "qkv"), (out, "out")):
+        _bf16_dev(t, n)
+    if kv.dtype != torch.uint8 or not kv.is_cuda or not kv.is_contiguous():
+        raise OmniAttnError(EINVAL, "kv must be a contiguous uint8 device tensor of FP8 slots")
+    for t, n in ((pos, "pos"), (slots, "slots"), (indptr, "indptr"), (pages, "pages")):
+        _i32_dev(t, n)
+    _check(load().omni_lm_rope_attend_fp8(_ptr(qkv), _ptr(pos), _ptr(slots), _ptr(kv), _ptr(indptr), _ptr(pages), page,
+                                          _ptr(out), heads, float(coef), float(scale), context, ctypes.byref(plan),
+                                          _ws(plan, workspace), _stream(stream)))
     return out
 
 

@@ -11,6 +11,7 @@
  */
 #include <stddef.h>
 #include <stdint.h>
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -288,6 +289,19 @@ static void check_head64_validation(void) {
     CHECK(omni_attn_decode_plan_init(0, 16, 8, 16, 600, 256, &p) == OMNI_ATTN_OK);
     CHECK(omni_qwen3_rope_attend(NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 16, NULL, 16, 8, 1e-6f, 1e6f, 0.1f,
                                  &p, NULL, NULL) == OMNI_ATTN_OK);
+  }
+  {
+    omni_attn_decode_plan p;
+    CHECK(omni_attn_decode_plan_init(4, 8, 8, 16, 600, 256, &p) == OMNI_ATTN_OK);
+    /* context; null slots; coef; a plan for other heads */
+    CHECK(omni_lm_rope_attend_fp8(kFake, kFake, kFake, kFake, kFake, kFake, 16, kFake, 8, -0.1f, 0.1f, 0, &p, kFake,
+                                  NULL) == OMNI_ATTN_EINVAL);
+    CHECK(omni_lm_rope_attend_fp8(kFake, kFake, NULL, kFake, kFake, kFake, 16, kFake, 8, -0.1f, 0.1f, 600, &p, kFake,
+                                  NULL) == OMNI_ATTN_EINVAL);
+    CHECK(omni_lm_rope_attend_fp8(kFake, kFake, kFake, kFake, kFake, kFake, 16, kFake, 8, NAN, 0.1f, 600, &p, kFake,
+                                  NULL) == OMNI_ATTN_EINVAL);
+    CHECK(omni_lm_rope_attend_fp8(kFake, kFake, kFake, kFake, kFake, kFake, 16, kFake, 16, -0.1f, 0.1f, 600, &p, kFake,
+                                  NULL) == OMNI_ATTN_EINVAL);
   }
 }
 

@@ -183,3 +183,90 @@ def test_fused_sweep(case):
     c = W.paged_decode_case(rows, hq, hk, lo, hi, page=page, seed=case, slack_pages=3)
     check_identical(c, chunk=chunk, seed=case,
                     what=f"fused case {case}: {hq}/{hk} page {page} rows {rows} len [{lo}, {hi}] chunk {chunk}")
+
+
+# ------------------------------------------------------ FP8 ring (PersonaPlex)
+
+COEF = float(np.float32(-np.log(10000.0) * 2.0 / 128))
+
+
+def ring_slots_of(c):
+    """The page-table slot of each row's ring index pos[n] % context."""
+    out = []
+    for n, p in enumerate(c.pos):
+        t = int(p) % c.context
+        out.append(c.pages[c.indptr[n] + t // c.page] * c.page + t % c.page)
+    return np.asarray(out, np.int32)
+
+
+def run_both_fp8(c, chunk=0, group_heads=0):
+    heads = c.hq
+    slots = ring_slots_of(c)
+    kv0 = c.kv.copy()
+    kv0[slots] = 0x7F  # E4M3 NaN in K and V, NaN scales, where the new keys go
+    plan = oa.decode_plan(c.rows, heads, heads, c.page, int(c.lens().max()), chunk)
+    plan.group_heads = group_heads
+    ws = oa.workspace_for(plan)
+    pos, sl, seq = dev_i32(c.pos), dev_i32(slots), dev_i32(c.seq)
+    indptr, pages = dev_i32(c.indptr), dev_i32(c.pages)
+    res = []
+    for fused in (False, True):
+        qkv = dev_bits(c.qkv)
+        kv = torch.from_numpy(np.ascontiguousarray(kv0)).cuda()
+        out = torch.full((c.rows, heads * 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+        if fused:
+            oa.lm_rope_attend_fp8(qkv, pos, sl, kv, indptr, pages, c.page, out, heads, COEF, c.scale, c.context, plan,
+                                  ws)
+        else:
+            oa.lm_rope(qkv, pos, sl, kv, c.rows, heads, COEF)
+            oa.lm_attend_fp8(qkv, kv, pos, seq, 0, indptr, pages, c.page, out, heads, c.scale, c.context, plan, ws)
+        torch.cuda.synchronize()
+        res.append((host_bits(out), kv.cpu().numpy(), host_bits(qkv)))
+    return res[0], res[1], (slots, kv0)
+
+
+def check_identical_fp8(c, chunk=0, group_heads=0, what=""):
+    (o_s, kv_s, _), (o_f, kv_f, q_f), extra = run_both_fp8(c, chunk, group_heads)
+    assert np.all(np.isfinite(bits_to_f64(o_f))), f"{what}: non-finite output"
+    assert np.array_equal(o_f, o_s), f"{what}: output differs from lm_rope + lm_attend_fp8"
+    assert np.array_equal(kv_f, kv_s), f"{what}: FP8 cache differs"
+    assert np.array_equal(q_f, c.qkv), f"{what}: qkv was written"
+    return o_f, kv_f, extra
+
+
+@pytest.mark.parametrize("heads,page,gh", [(8, 16, 0), (8, 12, 2), (8, 1, 1), (32, 16, 0), (32, 16, 8), (16, 4, 4)])
+def test_fused_fp8_equals_separate(heads, page, gh):
+    """Rows of 1 .. 900 tokens over a 600-slot ring: rows past the ring take
+    their new key at ring index pos % 600, in the middle of their keys; the
+    others at their last key."""
+    c = W.fp8_ring_case(40, heads, 1, 900, 600, page=page, seed=heads + page + gh, slack_pages=4)
+    check_identical_fp8(c, chunk=128, group_heads=gh, what=f"fp8 {heads} heads page {page} gh {gh}")
+
+
+def test_fused_fp8_config3_full_size_vs_oracle(oracle):
+    """Config 3's shape over FP8 slots (128 rows, 32 heads, U[100, 3000], ring
+    3000): fused = separate bit for bit, and within tolerance of the oracle's
+    lm_rope + lm_attend_fp8 chain; the scatter's bytes equal the oracle's."""
+    c = W.fp8_ring_case(128, 32, 100, 3000, 3000, seed=3000, slack_pages=4)
+    o_f, kv_f, (slots, kv0) = check_identical_fp8(c, what="config 3 fp8")
+    q_want, kv_want = oracle.lm_rope(c.qkv, c.pos, slots, kv0, 32, COEF)
+    want = oracle.lm_attend_fp8(q_want, kv_want, c.pos, c.seq, 0, c.indptr, c.pages, 16, 32, c.scale, 3000,
+                                nthreads=16)
+    assert_close(o_f, want, what="config 3 fp8 fused vs oracle chain")
+    untouched = np.setdiff1d(np.arange(kv_f.shape[0]), slots)
+    assert np.array_equal(kv_f[untouched], kv0[untouched])
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_fused_fp8_sweep(case):
+    rng = np.random.default_rng(4000 + case)
+    heads = int(rng.choice([2, 4, 8, 16, 32]))
+    page = int(rng.choice(PAGES))
+    rows = int(rng.integers(1, 41))
+    lo = int(rng.integers(1, 600))
+    hi = lo + int(rng.integers(0, 1200))
+    context = int(rng.integers(1, hi + 1))
+    chunk = int(rng.choice([0, 128, 256, 512]))
+    c = W.fp8_ring_case(rows, heads, lo, hi, context, page=page, seed=case, slack_pages=3)
+    check_identical_fp8(c, chunk=chunk, what=f"fp8 fused case {case}: {heads} heads page {page} rows {rows} "
+                        f"len [{lo}, {hi}] ctx {context} chunk {chunk}")
