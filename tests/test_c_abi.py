@@ -48,7 +48,7 @@ def test_kernel_index_arithmetic_on_the_host():
 def test_host_code_under_asan_ubsan():
     if not os.path.exists(os.path.join(ROOT, "pega-omni_amd", "_build", "decode.hip.o")):
         pytest.skip("kernel objects are not built")
-    _make("_build/abi_check_san", "_build/host_fuzz_san")
+    _make(*(os.path.join(CDIR, "_build", t) for t in ("abi_check_san", "host_fuzz_san")))
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1", UBSAN_OPTIONS="halt_on_error=1")
     for exe, want in (("abi_check_san", "checks passed"), ("host_fuzz_san", "cases")):
         r = subprocess.run([os.path.join(CDIR, "_build", exe)], capture_output=True, text=True, env=env)
