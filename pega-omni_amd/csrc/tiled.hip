@@ -234,8 +234,10 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   const int r = wave * 32 + j;
   const int p = r / G, head = kvh * G + r % G;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  // Waves outside this workgroup's half only load K/V tiles (wave-uniform).
-  const bool active = half < 0 || (wave_u >> 2) == half;
+  // Waves outside this workgroup's half, and waves none of whose 32 rows is a
+  // position of the tile (a short last tile), only load K/V tiles and meet
+  // the barriers (wave-uniform).
+  const bool active = (half < 0 || (wave_u >> 2) == half) && (32 * wave_u) / G < t.nq;
   const bool row_ok = p < t.nq && active;
   int lim;  // keys this row sees
   if constexpr (PAGED)
@@ -477,13 +479,15 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
     __syncthreads();
   };
-  // A wave outside the half: the same loads and barriers, no compute.
+  // A wave that computes nothing: the same loads (its rows of every K/V
+  // tile, with the page ids a tile ahead) and barriers.
   auto load_step = [&](int st, bf16_t* nxt) {
     if (st + 1 < s_hi) issue_tile((st + 1) * kBN, nxt);
+    if (page_wave && st + 2 < s_hi) next_pid = wave_page((st + 2) * kBN);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
   };
-  if (HALVES && !active) {
+  if (!active) {
     for (int st = s_lo; st < s_hi; st += 2) {
       load_step(st, smem1);
       if (st + 1 < s_hi) load_step(st + 1, smem0);
@@ -498,6 +502,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
   // Register e of block md is dim 32 md + 8 (e / 4) + 4 h + e % 4.
   l += xor_lane(l, 32);
   if (chunk >= 0) {  // a chunk's partial: unnormalised O with its base m and sum l, for dit_combine
+    if (!row_ok) return;  // dit_combine reads the tile's positions only
     float* seg = a.ws + (int64_t)((idx - a.split_from) * a.split_k + chunk) * (kBM * (kHead + 2));
 #pragma unroll
     for (int md = 0; md < 4; ++md)
