@@ -182,6 +182,17 @@ def time_steps(run_step, steps, warmup, stream, per_launch=None):
     return ms, launch_ms
 
 
+def graph_launch_us(call, steps, warmup, stream, n=20):
+    """One small launch as a replayed HIP graph of `n` back-to-back launches:
+    device time per launch without the host's launch path between them (the
+    engines replay their decode step as a graph)."""
+    def step(s, ev):
+        for _ in range(n):
+            call(s)
+
+    return graph_step_ms(step, steps, warmup, stream) * 1e3 / n
+
+
 def graph_step_ms(run_step, steps, warmup, stream):
     """The step captured once into a HIP graph and replayed, as the engines run
     decode (one graph per batch bucket): ms per replay over `steps` replays
@@ -438,7 +449,8 @@ def rope_bench(stream, steps, warmup):
     """Rotary + K/V scatter, one launch per step, at the engines' shapes:
     config 2 decode rows (qwen3_rope), a config-3 tick (lm_rope into FP8
     slots), config 4's prefill rows (qwen3_rope) and both HiDream CFG rows
-    (hidream_qk_rope). Bytes: qkv read, q and K/V written, weights, indices."""
+    (hidream_qk_rope). Bytes: qkv read, q and K/V written, weights, indices.
+    `graph_us`: the same launch timed as a replayed HIP graph of 20 launches."""
     import numpy as np
     import torch
 
@@ -458,9 +470,11 @@ def rope_bench(stream, steps, warmup):
                 ev[0][1].record(s)
 
         ms, launch_ms = time_steps(step, steps * 5, warmup, stream, per_launch=1)
+        g_us = graph_launch_us(call, steps, warmup, stream)
         res[name] = dict(rows=rows, heads=f"{hq}q/{hk}kv", bytes=bytes_, launch_us=round(launch_ms * 1e3, 2),
                          gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1),
-                         frac=round(bytes_ / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+                         frac=round(bytes_ / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         graph_us=round(g_us, 2), graph_gbs=round(bytes_ / (g_us * 1e-6) / 1e9, 1))
 
     rng = np.random.default_rng(7)
     w = torch.ones(128, dtype=torch.bfloat16, device="cuda")
@@ -502,7 +516,8 @@ def short_bench(stream, steps, warmup):
     250-slot rings) and the rotary + ring write before it, a 3000-slot prefix
     copy over FP8 slots, the codec decoder's fused attention (64 sessions, 16
     heads, a full 72-frame ring) and the depformer's last step (128 sessions,
-    16 heads, step 7). Bytes: K/V rows read once per (row, head), q, out, writes."""
+    16 heads, step 7). Bytes: K/V rows read once per (row, head), q, out, writes.
+    `graph_us`: the same launch timed as a replayed HIP graph of 20 launches."""
     import numpy as np
     import torch
 
@@ -523,8 +538,10 @@ def short_bench(stream, steps, warmup):
                 ev[0][1].record(s)
 
         ms, launch_ms = time_steps(step, steps * 5, warmup, stream, per_launch=1)
+        g_us = graph_launch_us(call, steps, warmup, stream)
         res[name] = dict(bytes=bytes_, launch_us=round(launch_ms * 1e3, 2),
-                         gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1))
+                         gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1),
+                         graph_us=round(g_us, 2), graph_gbs=round(bytes_ / (g_us * 1e-6) / 1e9, 1))
 
     # code predictor: hq16/hk8, one row per session at position 15
     rows, hq, hk = 64, 16, 8
