@@ -97,7 +97,9 @@ class DecodeBench:
                                  pages=i32(pages),
                                  out=torch.empty(case.rows, case.hq * 128, dtype=torch.bfloat16, device="cuda")))
         c0 = self.cases[0]
-        self.plan = oa.decode_plan(c0.rows, c0.hq, c0.hk, c0.page, c["len_hi"] if not self.lm else c["context"], chunk)
+        max_len = c["len_hi"] if not self.lm else c["context"]
+        self.plan = (oa.decode_plan_fp8(c0.rows, c0.hq, c0.page, max_len, chunk) if fp8 else
+                     oa.decode_plan(c0.rows, c0.hq, c0.hk, c0.page, max_len, chunk))
         self.plan.group_heads = group_heads
         self.ws = oa.workspace_for(self.plan)
         self.bytes_per_layer = [W.fp8_kv_bytes(cs) if fp8 else cs.kv_bytes() for cs in self.cases]

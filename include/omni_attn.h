@@ -68,6 +68,16 @@ typedef struct omni_attn_decode_plan {
 int omni_attn_decode_plan_init(int rows, int hq, int hk, int page, int max_len, int chunk_hint,
                                omni_attn_decode_plan* plan);
 
+/* The plan for lm_attend over its FP8 slots (omni_lm_attend_fp8 and
+ * omni_lm_rope_attend_fp8; crates/omni-personaplex/kernels/lm.cu:273-290 has
+ * no plan, its launch is fixed per bucket by crates/omni-personaplex/src/helium.rs:256-260):
+ * the plan omni_attn_decode_plan_init makes with hq = hk = heads, except that
+ * chunk_hint <= 0 picks the split size for the FP8 kernel's shape (up to 8
+ * heads per workgroup): the largest of 1024 / 768 / 512 / 384 keys that still
+ * gives 2048 workgroups of 8 heads, else 256. */
+int omni_attn_decode_plan_init_fp8(int rows, int heads, int page, int max_len, int chunk_hint,
+                                   omni_attn_decode_plan* plan);
+
 /* Replaces `qwen3_attend` (crates/omni-qwen3/kernels/qwen3.cu:234-240): row n
  * of sequence s = ragged ? seq[n] : n attends to pos[n] + 1 keys. Arguments in
  * the reference's order, then the plan's rows, workspace and stream.

@@ -27,6 +27,7 @@ ETABLE = -5
 
 EXPORTS = (
     "omni_attn_decode_plan_init",
+    "omni_attn_decode_plan_init_fp8",
     "omni_qwen3_attend",
     "omni_qwen3_attend_noalloc",
     "omni_lm_attend",
@@ -120,6 +121,7 @@ def load(path: str | None = None):
     pplan = ctypes.POINTER(PrefillPlan)
     sig = {
         "omni_attn_decode_plan_init": [i32, i32, i32, i32, i32, i32, dplan],
+        "omni_attn_decode_plan_init_fp8": [i32, i32, i32, i32, i32, dplan],
         "omni_qwen3_attend": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P, P],
         "omni_qwen3_attend_noalloc": [P, P, P, P, i32, P, P, i32, P, i32, i32, f32, dplan, P],
         "omni_lm_attend": [P, P, P, P, i32, P, P, i32, P, i32, f32, i32, dplan, P, P],
@@ -223,6 +225,13 @@ def _ws(plan, workspace):
 def decode_plan(rows: int, hq: int, hk: int, page: int, max_len: int, chunk: int = 0) -> DecodePlan:
     plan = DecodePlan()
     _check(load().omni_attn_decode_plan_init(rows, hq, hk, page, max_len, chunk, ctypes.byref(plan)))
+    return plan
+
+
+def decode_plan_fp8(rows: int, heads: int, page: int, max_len: int, chunk: int = 0) -> DecodePlan:
+    """The plan for lm_attend over FP8 slots (split size picked for the FP8 kernel)."""
+    plan = DecodePlan()
+    _check(load().omni_attn_decode_plan_init_fp8(rows, heads, page, max_len, chunk, ctypes.byref(plan)))
     return plan
 
 

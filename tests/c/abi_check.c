@@ -51,6 +51,10 @@ static void check_decode_plan(void) {
   CHECK(p.workspace_bytes == (p.splits > 1 ? 128LL * 32 * p.splits * 129 * 4 : 0));
   CHECK(p.group_heads == 0);
   CHECK(omni_attn_decode_plan_init(4, 16, 8, 16, 1000, 256, &p) == OMNI_ATTN_OK && p.chunk == 256 && p.splits == 4);
+  /* the FP8 plan: split size for the FP8 kernel, otherwise the same plan */
+  CHECK(omni_attn_decode_plan_init_fp8(128, 32, 16, 3000, 0, &p) == OMNI_ATTN_OK && p.chunk == 768 && p.splits == 4 &&
+        p.hq == 32 && p.hk == 32 && p.workspace_bytes == 128LL * 32 * 4 * 129 * 4);
+  CHECK(omni_attn_decode_plan_init_fp8(4, 0, 16, 100, 0, &p) == OMNI_ATTN_EINVAL);
   /* documented rejections */
   CHECK(omni_attn_decode_plan_init(4, 16, 6, 16, 100, 0, &p) == OMNI_ATTN_EINVAL);        /* hq % hk */
   CHECK(omni_attn_decode_plan_init(4, 16, 2, 16, 100, 0, &p) == OMNI_ATTN_EUNSUPPORTED);  /* G = 8 */

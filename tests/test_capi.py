@@ -41,6 +41,35 @@ def test_decode_plan_shapes():
     assert p2.chunk == 256 and p2.splits == 4
 
 
+@pytest.mark.parametrize("rows,chunk", [(32, 256), (64, 384), (128, 768), (256, 1024), (1, 256)])
+def test_decode_plan_fp8_picks_the_fp8_split(rows, chunk):
+    """The FP8 plan's split size: the largest of 1024/768/512/384 keys giving
+    >= 2048 workgroups of 8 heads at full length (rows x heads / 8 x splits),
+    else 256; everything else as decode_plan with hq = hk = heads."""
+    p = oa.decode_plan_fp8(rows, 32, 16, 3000)
+    assert p.chunk == chunk
+    splits = -(-3000 // chunk)
+    assert (p.rows, p.hq, p.hk, p.page, p.max_len, p.splits) == (rows, 32, 32, 16, 3000, splits)
+    wgs = [rows * 4 * -(-3000 // c) for c in (1024, 768, 512, 384)]
+    assert chunk == next((c for c, w in zip((1024, 768, 512, 384), wgs) if w >= 2048), 256)
+    assert p.workspace_bytes == (rows * 32 * splits * 129 * 4 if splits > 1 else 0)
+    q = oa.decode_plan(rows, 32, 32, 16, 3000, chunk=chunk)
+    assert bytes(p) == bytes(q)  # the same plan as the bf16 init at that chunk
+    assert oa.decode_plan_fp8(rows, 32, 16, 3000, chunk=512).chunk == 512  # a hint is kept
+
+
+@pytest.mark.parametrize("args,code", [
+    ((4, 0, 16, 100, 0), oa.EINVAL),        # heads
+    ((4, 8, 0, 100, 0), oa.EINVAL),         # page
+    ((4, 8, 16, 0, 0), oa.EINVAL),          # max_len
+    ((4, 8, 16, 100, 96), oa.EINVAL),       # chunk not a multiple of 128
+])
+def test_decode_plan_fp8_rejects(args, code):
+    with pytest.raises(oa.OmniAttnError) as e:
+        oa.decode_plan_fp8(*args)
+    assert e.value.code == code
+
+
 @pytest.mark.parametrize("args,code", [
     ((4, 16, 6, 16, 100, 0), oa.EINVAL),        # hq not a multiple of hk
     ((4, 16, 2, 16, 100, 0), oa.EUNSUPPORTED),  # G = 8 not implemented in decode

@@ -89,7 +89,7 @@ def test_fp8_full_config3(oracle):
     qkv = torch.randn(c.rows, 3 * heads * 128, device="cuda", generator=gen).to(torch.bfloat16)
     c.qkv = host_bits(qkv)
     c.kv = kv8.cpu().numpy()
-    plan = oa.decode_plan(c.rows, heads, heads, 16, 3000)
+    plan = oa.decode_plan_fp8(c.rows, heads, 16, 3000)  # the FP8 plan's split size (768 keys here)
     out = torch.zeros(c.rows, heads * 128, dtype=torch.bfloat16, device="cuda")
     oa.lm_attend_fp8(qkv, kv8, dev_i32(c.pos), dev_i32(c.seq), 0, dev_i32(c.indptr), dev_i32(c.pages), 16, out,
                      heads, c.scale, 3000, plan, oa.workspace_for(plan))
