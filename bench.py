@@ -848,7 +848,7 @@ def main():
             extra["config5_mha"] = dit_bench(stream, args.steps, args.warmup, hk=32)
             # the reference's signature (no workspace): the last round's tiles run as row halves
             extra["config5_no_workspace"] = dit_bench(stream, args.steps, args.warmup, split=False)
-    if args.only in (0, 5, 10):
+    if args.only in (0, 10):
         extra["hidream_published_shape"] = published_shape_bench(stream, args.steps, args.warmup)
     # The MFMA legs against the ceiling random operands reach on this card (the
     # clock under full MFMA load falls as operand bits toggle), beside `frac`

@@ -532,8 +532,13 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
 
 // Merge the split_k chunk partials of each split DiT item into its output
 // rows: one workgroup per (item, 16 packed rows), 16 threads per row, 8 dims
-// each (two 16-byte partial loads per chunk).
+// each (two 16-byte partial loads per chunk). Two passes over the chunks, the
+// row's max base, then the weighted sums, each issuing the loads of
+// kCombineBatch chunks before using them (clamped to the last chunk, the
+// extra ones unused), so a pass costs one memory round trip per batch rather
+// than one per chunk.
 constexpr int kCombineRows = 16;
+constexpr int kCombineBatch = 8;
 
 __global__ __launch_bounds__(256) void dit_combine(TiledArgs a, int ntiles) {
   const int idx = a.split_from + blockIdx.x;
@@ -544,26 +549,43 @@ __global__ __launch_bounds__(256) void dit_combine(TiledArgs a, int ntiles) {
   const int p = r / G, head = kvh * G + r % G;
   if (p >= nq) return;
   constexpr int kSeg = kBM * (kHead + 2);
-  const float* seg0 = a.ws + (int64_t)(blockIdx.x * a.split_k) * kSeg;
+  const int nk = a.split_k;
+  const float* seg0 = a.ws + (int64_t)(blockIdx.x * nk) * kSeg;
+  const float* ml0 = seg0 + kBM * kHead + 2 * r;  // chunk c's (m, l) at ml0 + c * kSeg
   float top = -INFINITY;
-  for (int c = 0; c < a.split_k; ++c) top = fmaxf(top, seg0[c * kSeg + kBM * kHead + 2 * r]);
+  for (int c0 = 0; c0 < nk; c0 += kCombineBatch) {
+    float m[kCombineBatch];
+#pragma unroll
+    for (int i = 0; i < kCombineBatch; ++i) m[i] = ml0[min(c0 + i, nk - 1) * kSeg];
+#pragma unroll
+    for (int i = 0; i < kCombineBatch; ++i) top = fmaxf(top, m[i]);  // a repeated chunk changes no max
+  }
   float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float den = 0.f;
-  for (int c = 0; c < a.split_k; ++c) {
-    const float* seg = seg0 + c * kSeg;
-    const float2 ml = *reinterpret_cast<const float2*>(seg + kBM * kHead + 2 * r);
-    const float w = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - top);
-    den = fmaf(ml.y, w, den);
-    const float4 v0 = *reinterpret_cast<const float4*>(seg + r * kHead + d0);
-    const float4 v1 = *reinterpret_cast<const float4*>(seg + r * kHead + d0 + 4);
-    num[0] = fmaf(v0.x, w, num[0]);
-    num[1] = fmaf(v0.y, w, num[1]);
-    num[2] = fmaf(v0.z, w, num[2]);
-    num[3] = fmaf(v0.w, w, num[3]);
-    num[4] = fmaf(v1.x, w, num[4]);
-    num[5] = fmaf(v1.y, w, num[5]);
-    num[6] = fmaf(v1.z, w, num[6]);
-    num[7] = fmaf(v1.w, w, num[7]);
+  for (int c0 = 0; c0 < nk; c0 += kCombineBatch) {
+    float2 ml[kCombineBatch];
+    float4 v0[kCombineBatch], v1[kCombineBatch];
+#pragma unroll
+    for (int i = 0; i < kCombineBatch; ++i) {
+      const float* seg = seg0 + min(c0 + i, nk - 1) * kSeg;
+      ml[i] = *reinterpret_cast<const float2*>(seg + kBM * kHead + 2 * r);
+      v0[i] = *reinterpret_cast<const float4*>(seg + r * kHead + d0);
+      v1[i] = *reinterpret_cast<const float4*>(seg + r * kHead + d0 + 4);
+    }
+#pragma unroll
+    for (int i = 0; i < kCombineBatch; ++i) {
+      if (c0 + i >= nk) break;
+      const float w = ml[i].x == -INFINITY ? 0.f : fast_exp2(ml[i].x - top);
+      den = fmaf(ml[i].y, w, den);
+      num[0] = fmaf(v0[i].x, w, num[0]);
+      num[1] = fmaf(v0[i].y, w, num[1]);
+      num[2] = fmaf(v0[i].z, w, num[2]);
+      num[3] = fmaf(v0[i].w, w, num[3]);
+      num[4] = fmaf(v1[i].x, w, num[4]);
+      num[5] = fmaf(v1[i].y, w, num[5]);
+      num[6] = fmaf(v1[i].z, w, num[6]);
+      num[7] = fmaf(v1[i].w, w, num[7]);
+    }
   }
   // den = 0 only when no chunk saw a key: NaN, as the unsplit kernel stores.
   const float inv = 1.f / den;
