@@ -447,12 +447,12 @@ def published_shape_bench(stream, steps, warmup):
     return res
 
 
-def rope_bench(stream, steps, warmup):
+def rope_bench(stream, steps, warmup, graph=True):
     """Rotary + K/V scatter, one launch per step, at the engines' shapes:
     config 2 decode rows (qwen3_rope), a config-3 tick (lm_rope into FP8
     slots), config 4's prefill rows (qwen3_rope) and both HiDream CFG rows
     (hidream_qk_rope). Bytes: qkv read, q and K/V written, weights, indices.
-    `graph_us`: the same launch timed as a replayed HIP graph of 20 launches."""
+    `graph_us`: the same launch timed as a replayed HIP graph of 20 launches (not with --no-graph)."""
     import numpy as np
     import torch
 
@@ -472,7 +472,7 @@ def rope_bench(stream, steps, warmup):
                 ev[0][1].record(s)
 
         ms, launch_ms = time_steps(step, steps * 5, warmup, stream, per_launch=1)
-        g_us = graph_launch_us(call, steps, warmup, stream)
+        g_us = graph_launch_us(call, steps, warmup, stream) if graph else float("nan")
         res[name] = dict(rows=rows, heads=f"{hq}q/{hk}kv", bytes=bytes_, launch_us=round(launch_ms * 1e3, 2),
                          gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1),
                          frac=round(bytes_ / (launch_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -511,7 +511,7 @@ def rope_bench(stream, steps, warmup):
     return res
 
 
-def short_bench(stream, steps, warmup):
+def short_bench(stream, steps, warmup, graph=True):
     """The small attentions at engine shapes, one launch per step: the code
     predictor's qwen3_attend_dense (64 sessions at position 15 of a 16-slot
     workspace), Mimi's ring attention (128 sessions x 2 rows, 8 heads, full
@@ -519,7 +519,7 @@ def short_bench(stream, steps, warmup):
     copy over FP8 slots, the codec decoder's fused attention (64 sessions, 16
     heads, a full 72-frame ring) and the depformer's last step (128 sessions,
     16 heads, step 7). Bytes: K/V rows read once per (row, head), q, out, writes.
-    `graph_us`: the same launch timed as a replayed HIP graph of 20 launches."""
+    `graph_us`: the same launch timed as a replayed HIP graph of 20 launches (not with --no-graph)."""
     import numpy as np
     import torch
 
@@ -540,7 +540,7 @@ def short_bench(stream, steps, warmup):
                 ev[0][1].record(s)
 
         ms, launch_ms = time_steps(step, steps * 5, warmup, stream, per_launch=1)
-        g_us = graph_launch_us(call, steps, warmup, stream)
+        g_us = graph_launch_us(call, steps, warmup, stream) if graph else float("nan")
         res[name] = dict(bytes=bytes_, launch_us=round(launch_ms * 1e3, 2),
                          gbs=round(bytes_ / (launch_ms * 1e-3) / 1e9, 1),
                          graph_us=round(g_us, 2), graph_gbs=round(bytes_ / (g_us * 1e-6) / 1e9, 1))
@@ -938,12 +938,12 @@ def main():
         torch.cuda.empty_cache()
     if args.only in (0, 7):
         log("[bench] rotary + K/V scatter")
-        extra["rope"] = rope_bench(stream, args.steps, args.warmup)
+        extra["rope"] = rope_bench(stream, args.steps, args.warmup, graph=not args.no_graph)
         log(f"[bench] {extra['rope']}")
         torch.cuda.empty_cache()
     if args.only in (0, 8):
         log("[bench] dense and head-64 attentions")
-        extra["short"] = short_bench(stream, args.steps, args.warmup)
+        extra["short"] = short_bench(stream, args.steps, args.warmup, graph=not args.no_graph)
         log(f"[bench] {extra['short']}")
         torch.cuda.empty_cache()
     if args.only in (4, 5, 2, 6, 7, 8, 9, 10):
