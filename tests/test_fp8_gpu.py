@@ -24,6 +24,19 @@ def run_fp8(c, heads, chunk=0, max_len=None, group_heads=0):
     return host_bits(out)
 
 
+def run_fp8_planned(c, heads, max_len):
+    """omni_lm_attend_fp8 on the FP8 plan (omni_attn_decode_plan_init_fp8's
+    split size, the launch's own heads per workgroup)."""
+    plan = oa.decode_plan_fp8(c.rows, heads, c.page, max_len)
+    out = torch.zeros(c.rows, heads * 128, dtype=torch.bfloat16, device="cuda")
+    kv = torch.from_numpy(np.ascontiguousarray(c.kv)).cuda()
+    oa.lm_attend_fp8(dev_bits(c.qkv), kv, dev_i32(c.pos), dev_i32(c.seq), c.ragged, dev_i32(c.indptr),
+                     dev_i32(c.pages), c.page, out, heads, c.scale, c.context or (1 << 30), plan,
+                     oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    return host_bits(out), plan.chunk
+
+
 def oracle_fp8(oracle, c, heads):
     return oracle.lm_attend_fp8(c.qkv, c.kv, c.pos, c.seq, c.ragged, c.indptr, c.pages, c.page, heads, c.scale,
                                 c.context, nthreads=16)
@@ -35,6 +48,37 @@ def oracle_fp8(oracle, c, heads):
 def test_fp8_parity(oracle, heads, lo, hi, ctx, chunk):
     c = W.fp8_ring_case(7, heads, lo, hi, ctx, seed=heads * 7 + lo, slack_pages=3)
     assert_close(run_fp8(c, heads, chunk), oracle_fp8(oracle, c, heads), what=f"fp8 h{heads} ctx{ctx}")
+
+
+def device_fp8_case(rows, heads, seed):
+    """PersonaPlex rows (lengths U[100, 3000], ring 3000) with FP8 slots
+    quantized on the device, per (slot, head) scale max(amax / 448, 1e-12)."""
+    c = W.paged_decode_case(rows, heads, heads, 100, 3000, seed=seed, context=3000, values=None, slack_pages=3)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    slots = c.num_pages * c.page
+    kv8 = torch.empty(slots, W.fp8_slot_bytes(heads), dtype=torch.uint8, device="cuda")
+    for s0 in range(0, slots, 8192):
+        s1 = min(slots, s0 + 8192)
+        x = torch.randn(s1 - s0, 2 * heads, 128, device="cuda", generator=gen)
+        sc = torch.clamp(x.abs().amax(-1, keepdim=True) / 448.0, min=1e-12)
+        kv8[s0:s1, : 2 * heads * 128] = (x / sc).to(torch.float8_e4m3fn).view(torch.uint8).reshape(s1 - s0, -1)
+        kv8[s0:s1, 2 * heads * 128:] = sc.reshape(s1 - s0, -1).contiguous().view(torch.uint8)
+    qkv = torch.randn(c.rows, 3 * heads * 128, device="cuda", generator=gen).to(torch.bfloat16)
+    c.qkv = host_bits(qkv)
+    c.kv = kv8.cpu().numpy()
+    return c
+
+
+@pytest.mark.parametrize("rows,chunk", [(32, 256), (64, 384)])
+def test_fp8_plan_buckets(oracle, rows, chunk):
+    """The FP8 plan's split size at smaller PersonaPlex buckets (32 heads):
+    256 and 384 keys, with the launch's pick of 4 and 8 heads per workgroup
+    (the 128-session tick's 768 runs in test_fp8_full_config3), against the
+    oracle."""
+    c = device_fp8_case(rows, 32, seed=rows + 5)
+    got, picked = run_fp8_planned(c, 32, 3000)
+    assert picked == chunk
+    assert_close(got, oracle_fp8(oracle, c, 32), what=f"fp8 plan rows {rows}")
 
 
 @pytest.mark.parametrize("gh", [1, 2, 4, 8])
