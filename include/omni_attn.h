@@ -208,7 +208,11 @@ typedef struct omni_attn_prefill_plan {
   int32_t tile_rows; /* packed (position, head) rows per tile */
   int64_t work_bytes; /* bytes of the int32 work list the caller uploads */
   int32_t workgroups; /* grid of omni_attn_prefill_run */
-  int32_t reserved;
+  int32_t exact_p;    /* 0 (what plan_init sets): P rounded to bf16 for P.V, as the MFMA
+                         flash kernels of the reference do (hidream.cu:317-324); 1: P carried
+                         as two bf16 terms (hi + lo) through P.V, 16 significant bits, for
+                         qwen3_attend(ragged = 1)'s f32 P (qwen3.cu:160-176) at about 1.4x
+                         the time */
 } omni_attn_prefill_plan;
 
 /* Host: validate (seq_h, pos_h) for `rows` ragged rows and write the work list

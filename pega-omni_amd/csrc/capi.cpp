@@ -327,7 +327,7 @@ int omni_attn_prefill_plan_init(int rows, int hq, int hk, int page, const int32_
   const int64_t need = omni::kPrefillWorkHeader + 4 * items;
   plan->work_bytes = need * (int64_t)sizeof(int32_t);
   plan->workgroups = 0;
-  plan->reserved = 0;
+  plan->exact_p = 0;
   if (!work_h || need > work_cap)
     return fail(OMNI_ATTN_EWORKSPACE, "prefill_plan: work list needs %lld int32", (long long)need);
   // Item order: tiles by the keys they see, most first (a tile's time grows
@@ -373,11 +373,12 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
   const int64_t items = (int64_t)plan->tiles * (plan->hk > 0 ? plan->hk : 0);
   if (plan->tiles < 0 || (G != 1 && G != 2 && G != 4 && G != 8) || plan->page <= 0 ||
       plan->tile_rows != omni::kTiledRows || plan->workgroups != (items + omni::kXcds - 1) / omni::kXcds * omni::kXcds ||
-      plan->work_bytes != (omni::kPrefillWorkHeader + 4 * items) * (int64_t)sizeof(int32_t))
+      plan->work_bytes != (omni::kPrefillWorkHeader + 4 * items) * (int64_t)sizeof(int32_t) ||
+      (plan->exact_p != 0 && plan->exact_p != 1))
     return fail(OMNI_ATTN_EINVAL,
                 "prefill_run: plan is not one prefill_plan_init made (tiles=%d hq=%d hk=%d page=%d tile_rows=%d "
-                "workgroups=%d)",
-                plan->tiles, plan->hq, plan->hk, plan->page, plan->tile_rows, plan->workgroups);
+                "workgroups=%d exact_p=%d)",
+                plan->tiles, plan->hq, plan->hk, plan->page, plan->tile_rows, plan->workgroups, plan->exact_p);
   if (plan->tiles == 0) return ok();
   if (!qkv || !kv || !pos || !seq || !indptr || !pages || !out || !work)
     return fail(OMNI_ATTN_EINVAL, "prefill_run: null device pointer");
@@ -398,6 +399,7 @@ int omni_attn_prefill_run(const omni_attn_prefill_plan* plan, const void* qkv, c
   a.hq = plan->hq;
   a.hk = plan->hk;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.exact_p = plan->exact_p;
   const int rc = omni::launch_prefill(a, plan->workgroups, as_stream(stream));
   if (rc == -2) return fail(OMNI_ATTN_EUNSUPPORTED, "prefill_run: shape not implemented");
   if (rc != 0) return fail(OMNI_ATTN_ELAUNCH, "prefill_run: launch failed: %s", hipGetErrorString(omni::g_launch_status));

@@ -100,6 +100,8 @@ struct TiledArgs {
   // Row halves (dense, no split): the last `halved` items run as two
   // workgroups of kTiledRows / 2 packed rows each; 0 = none.
   int halved;
+  // Prefill with P carried as two bf16 terms (hi + lo) through P.V.
+  int exact_p;
 };
 
 // Packed (position, head) query rows per MFMA tile: one 8-wave workgroup, one per CU.

@@ -129,7 +129,7 @@ struct Tile {
   int64_t per_slot;          // paged: elements per slot
 };
 
-template <int G, bool PAGED, bool HALVES = false>
+template <int G, bool PAGED, bool HALVES = false, bool EXACT = false>
 __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items, int ntiles) {
   // DiT, XCD-aware order: workgroup id i runs on XCD i % 8; give each XCD a
   // contiguous block of work items so the tiles sharing one K/V head (and
@@ -467,6 +467,17 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = sc[ks_ >> 1][8 * (ks_ & 1) + e];
       const bf16x8 pf = pack8(pv);
+      // EXACT: P = P_hi + P_lo, both bf16 (P_lo = bf16(P - P_hi), P - P_hi
+      // exact in f32), and P.V as two MFMAs: P carries 16 significant bits
+      // into the accumulation instead of 8.
+      bf16x8 pfl;
+      if constexpr (EXACT) {
+        float pl[8];
+        widen8(__builtin_bit_cast(uint4, pf), pl);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pl[e] = pv[e] - pl[e];
+        pfl = pack8(pl);
+      }
 #pragma unroll
       for (int md = 0; md < 4; ++md) {
         const bf16_t* vb = vt + (v_lane ^ (32 * md)) + 16 * ks_ * kHead;
@@ -474,6 +485,7 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_attn(TiledArgs a, int items
         const bf16x4 hi = lds_read_tr(vb + 8 * kHead);
         const bf16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[md], 0, 0, 0);
+        if constexpr (EXACT) o[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pfl, o[md], 0, 0, 0);
       }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the next tile has landed
@@ -597,6 +609,19 @@ __global__ __launch_bounds__(256) void dit_combine(TiledArgs a, int ntiles) {
   *reinterpret_cast<uint4*>(a.out + b * a.out_bstride + ((int64_t)(q0 + p) * a.hq + head) * kHead + d0) = o;
 }
 
+// Prefill with exact_p set: the hi + lo P.V variant (prefill only; DiT rounds
+// P to bf16 as hidream.cu does). Returns whether it launched.
+template <int G, bool PAGED>
+bool launch_exact(const TiledArgs& a, int grid, int items, int ntiles, hipStream_t stream) {
+  if constexpr (PAGED) {
+    if (a.exact_p) {
+      tiled_attn<G, true, false, true><<<grid, kThreads, 0, stream>>>(a, items, ntiles);
+      return true;
+    }
+  }
+  return false;
+}
+
 template <bool PAGED>
 int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) {
   if (items <= 0) return 0;
@@ -610,7 +635,7 @@ int launch_tiled(const TiledArgs& a, int items, int ntiles, hipStream_t stream) 
   case G:                                                                                  \
     if (halves)                                                                            \
       tiled_attn<G, false, true><<<grid, kThreads, 0, stream>>>(a, items, ntiles);         \
-    else                                                                                   \
+    else if (!launch_exact<G, PAGED>(a, grid, items, ntiles, stream))                      \
       tiled_attn<G, PAGED><<<grid, kThreads, 0, stream>>>(a, items, ntiles);               \
     break;
     OMNI_CASE(1)

@@ -95,7 +95,7 @@ class PrefillPlan(ctypes.Structure):
         ("tile_rows", ctypes.c_int32),
         ("work_bytes", ctypes.c_int64),
         ("workgroups", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("exact_p", ctypes.c_int32),
     ]
 
 
@@ -338,8 +338,9 @@ class Prefill:
     work: object  # device int32 tensor
 
 
-def prefill_plan(rows, hq, hk, page, seq_h, pos_h, device="cuda") -> Prefill:
-    """Host plan of a ragged causal prefill; uploads the work list."""
+def prefill_plan(rows, hq, hk, page, seq_h, pos_h, device="cuda", exact_p=False) -> Prefill:
+    """Host plan of a ragged causal prefill; uploads the work list. exact_p:
+    P carried as two bf16 terms through P.V (qwen3_attend's f32 P, ~1.4x the time)."""
     import numpy as np
     import torch
 
@@ -356,6 +357,7 @@ def prefill_plan(rows, hq, hk, page, seq_h, pos_h, device="cuda") -> Prefill:
     _check(L.omni_attn_prefill_plan_init(rows, hq, hk, page, seq_a.ctypes.data_as(ctypes.c_void_p),
                                          pos_a.ctypes.data_as(ctypes.c_void_p),
                                          work_h.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(plan)))
+    plan.exact_p = 1 if exact_p else 0
     return Prefill(plan, torch.from_numpy(work_h).to(device))
 
 

@@ -38,6 +38,7 @@ _Static_assert(offsetof(omni_attn_decode_plan, workspace_bytes) == 32, "decode p
 _Static_assert(sizeof(omni_attn_prefill_plan) == 40, "prefill plan size");
 _Static_assert(offsetof(omni_attn_prefill_plan, work_bytes) == 24, "prefill plan work_bytes");
 _Static_assert(offsetof(omni_attn_prefill_plan, workgroups) == 32, "prefill plan workgroups");
+_Static_assert(offsetof(omni_attn_prefill_plan, exact_p) == 36, "prefill plan exact_p");
 
 /* A non-null address no call below dereferences: every call that receives it
  * fails validation before touching device memory. */
@@ -154,6 +155,7 @@ static void check_prefill_plan(void) {
   int32_t* work = (int32_t*)malloc((size_t)p.work_bytes);
   CHECK(work != NULL);
   CHECK(omni_attn_prefill_plan_init(kRows, 32, 8, 16, seq, pos, work, p.work_bytes / 4, &p) == OMNI_ATTN_OK);
+  CHECK(p.exact_p == 0); /* P rounded to bf16 unless the caller sets exact_p = 1 */
   CHECK(p.rows == kRows && p.hq == 32 && p.hk == 8 && p.tile_rows == 256);
   /* header: XCD ranges cover every item once, in order, widths differ by <= 1 */
   const int items = tiles * 8;

@@ -331,11 +331,13 @@ def test_prefill_rejects_bad_rows_and_plans():
     # (too few workgroups would skip items silently).
     for field, value in [("page", 0), ("workgroups", 0), ("workgroups", good.workgroups - 8),
                          ("workgroups", good.workgroups + 8), ("tiles", good.tiles + 1), ("tile_rows", 128),
-                         ("hq", 8 * 16), ("hq", 8 * 3), ("work_bytes", good.work_bytes - 4)]:
+                         ("hq", 8 * 16), ("hq", 8 * 3), ("work_bytes", good.work_bytes - 4),
+                         ("exact_p", 2), ("exact_p", -1)]:
         bad = oa.PrefillPlan.from_buffer_copy(good)
         setattr(bad, field, value)
         assert L.omni_attn_prefill_run(ctypes.byref(bad), f, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL, field
     assert L.omni_attn_prefill_run(ctypes.byref(good), odd, f, f, f, f, f, f, 0.1, f, None) == oa.EINVAL
+    assert good.exact_p == 0  # plan_init's default: P rounded to bf16
 
 
 def test_rows_push_keeps_positions_and_slots_in_int32():

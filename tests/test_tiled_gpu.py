@@ -12,8 +12,8 @@ from refs import bits_to_f64
 pytestmark = pytest.mark.gpu
 
 
-def run_prefill(c):
-    pf = oa.prefill_plan(c.rows, c.hq, c.hk, c.page, c.seq, c.pos)
+def run_prefill(c, exact_p=False):
+    pf = oa.prefill_plan(c.rows, c.hq, c.hk, c.page, c.seq, c.pos, exact_p=exact_p)
     out = torch.zeros(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
     oa.prefill_run(pf, dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), dev_i32(c.indptr),
                    dev_i32(c.pages), out, c.scale)
@@ -82,6 +82,13 @@ def test_prefill_config4_own_draw(oracle):
                     dev_i32(c.pages), c.page, out, c.hq, c.hk, c.scale, plan, oa.workspace_for(plan))
     torch.cuda.synchronize()
     assert_close(got, host_bits(out), what="config4 prefill vs decode, every row")
+    # The plan's exact_p (P as bf16 hi + lo, the reference's f32-P numerics):
+    # every row against the oracle and, nearly bit for bit, the decode kernel.
+    ex = run_prefill(c, exact_p=True)
+    mx, mn = assert_close(ex, want, what=f"config4 exact_p all {c.rows} rows vs oracle")
+    print(f"config4 exact_p vs oracle: max-abs {mx:.3g} mean-abs {mn:.3g}")
+    same = float(np.mean(ex == host_bits(out)))
+    assert same >= 0.99, f"exact_p prefill and the f32-P decode kernel agree on {same:.4f} of elements"
 
 
 def run_dense(c, b_all=True):
@@ -320,6 +327,48 @@ def test_prefill_long_sequence(oracle):
     sub = W.PagedCase(hq=32, hk=8, page=c.page, pos=c.pos[pick], seq=c.seq[pick], ragged=1, indptr=c.indptr,
                       pages=c.pages, num_pages=c.num_pages, qkv=c.qkv[pick], kv=c.kv)
     assert_close(got[pick], oracle_paged(oracle, sub), what="long prefill, first and last rows")
+
+
+@pytest.mark.parametrize("hq,hk,page", [(32, 8, 16), (16, 16, 16), (16, 8, 12), (64, 8, 16), (8, 4, 3)])
+def test_prefill_exact_p_parity(oracle, hq, hk, page):
+    """The plan's exact_p (P carried as two bf16 terms through P.V) on every
+    query-head group, paged through powers of two and not, against the oracle."""
+    c = W.ragged_prefill_case(3, hq, hk, 1, 300, 0, 200, page=page, seed=hq + hk + page)
+    assert_close(run_prefill(c, exact_p=True), oracle_paged(oracle, c), what=f"prefill exact_p {hq}/{hk} page {page}")
+
+
+@pytest.mark.parametrize("seed", [29, 31])
+def test_prefill_exact_p_is_the_f32_p_kernel(seed):
+    """With exact_p the MFMA prefill keeps P to 16 significant bits (hi + lo
+    bf16), the precision qwen3_attend(ragged = 1)'s f32 P reaches in its
+    bf16 output: it agrees bit for bit with the split-K decode kernel (f32 P)
+    on >= 99% of elements, differs by at most one bf16 ulp (or 2^-15 near zero)
+    elsewhere, and its
+    error against f64 SDPA is the decode kernel's (mean within 5%), below the
+    bf16-P prefill's."""
+    from refs import paged_truth
+    from gpu_util import bits_f32
+
+    c = W.ragged_prefill_case(2, 32, 8, 300, 700, 0, 200, seed=seed)
+    ex, pre = run_prefill(c, exact_p=True), run_prefill(c)
+    plan = oa.decode_plan(c.rows, c.hq, c.hk, c.page, int(c.pos.max()) + 1)
+    out = torch.zeros(c.rows, c.hq * 128, dtype=torch.bfloat16, device="cuda")
+    oa.qwen3_attend(dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), 1, dev_i32(c.indptr),
+                    dev_i32(c.pages), c.page, out, c.hq, c.hk, c.scale, plan, oa.workspace_for(plan))
+    torch.cuda.synchronize()
+    dec = host_bits(out)
+    assert np.mean(ex == dec) >= 0.99
+    fe, fd = bits_f32(ex).astype(np.float64), bits_f32(dec).astype(np.float64)
+    from refs import bf16_ulp
+    # Beyond the rounding step the two f32 results differ by summation order
+    # and P's 17th bit, a few 2^-24 of sum p |v| / l (< 1): 2^-15 absolute
+    # covers outputs near zero, where one ulp is smaller than that.
+    assert np.all(np.abs(fe - fd) <= bf16_ulp(np.maximum(np.abs(fe), np.abs(fd))) + 2.0 ** -15)
+    truth = paged_truth(c).reshape(c.rows, -1)
+    e_ex, e_dec = np.abs(fe - truth), np.abs(fd - truth)
+    e_pre = np.abs(bits_f32(pre).astype(np.float64) - truth)
+    assert e_ex.mean() <= 1.05 * e_dec.mean(), (e_ex.mean(), e_dec.mean())
+    assert e_ex.mean() < e_pre.mean(), (e_ex.mean(), e_pre.mean())
 
 
 def test_prefill_error_against_f64_truth_is_near_the_f32_p_kernels():
