@@ -23,6 +23,8 @@
 //     LDS and the V^T operand at exactly those keys comes from two transposing
 //     LDS reads (ds_read_b64_tr_b16) per MFMA.
 // LDS layouts keep the MFMA operand reads conflict-free (see kTileElems).
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -682,7 +684,13 @@ int dit_halves(const TiledArgs& a, int batch, int resident) {
 
 // With `resident` workgroups in flight (one per CU), items - items % resident
 // run whole and the rest each split into resident / (items % resident) key
-// chunks, so the last round is full instead of a fraction.
+// chunks, so the last round is full instead of a fraction; but no chunk of
+// fewer than kMinChunkTiles key tiles, counted on q_len (the key count is on
+// the device; DiT attends over about as many keys as queries): a shorter chunk
+// is mostly prologue and partial writes, and every chunk is one more partial
+// for dit_combine to merge.
+constexpr int kMinChunkTiles = 4;
+
 void dit_split(const TiledArgs& a, int batch, int resident, int* items, int* split_from, int* split_k) {
   const int G = a.hq / a.hk;
   const int ntiles = (a.q_len + kBM / G - 1) / (kBM / G);
@@ -693,8 +701,9 @@ void dit_split(const TiledArgs& a, int batch, int resident, int* items, int* spl
   if (resident <= 0 || n <= 0 || n > (1LL << 30)) return;
   const int rem = (int)(n % resident);
   if (rem == 0 || resident / rem < 2) return;
+  const int chunks = std::min(resident / rem, std::max(2, (a.q_len + kBN - 1) / kBN / kMinChunkTiles));
   *split_from = (int)n - rem;
-  *split_k = resident / rem;
+  *split_k = chunks;
 }
 
 }  // namespace omni
