@@ -199,12 +199,13 @@ def ring_slots_of(c):
     return np.asarray(out, np.int32)
 
 
-def run_both_fp8(c, chunk=0, group_heads=0):
+def run_both_fp8(c, chunk=0, group_heads=0, fp8_plan=False):
     heads = c.hq
     slots = ring_slots_of(c)
     kv0 = c.kv.copy()
     kv0[slots] = 0x7F  # E4M3 NaN in K and V, NaN scales, where the new keys go
-    plan = oa.decode_plan(c.rows, heads, heads, c.page, int(c.lens().max()), chunk)
+    plan = (oa.decode_plan_fp8(c.rows, heads, c.page, int(c.lens().max()), chunk) if fp8_plan else
+            oa.decode_plan(c.rows, heads, heads, c.page, int(c.lens().max()), chunk))
     plan.group_heads = group_heads
     ws = oa.workspace_for(plan)
     pos, sl, seq = dev_i32(c.pos), dev_i32(slots), dev_i32(c.seq)
@@ -225,8 +226,8 @@ def run_both_fp8(c, chunk=0, group_heads=0):
     return res[0], res[1], (slots, kv0)
 
 
-def check_identical_fp8(c, chunk=0, group_heads=0, what=""):
-    (o_s, kv_s, _), (o_f, kv_f, q_f), extra = run_both_fp8(c, chunk, group_heads)
+def check_identical_fp8(c, chunk=0, group_heads=0, what="", fp8_plan=False):
+    (o_s, kv_s, _), (o_f, kv_f, q_f), extra = run_both_fp8(c, chunk, group_heads, fp8_plan)
     assert np.all(np.isfinite(bits_to_f64(o_f))), f"{what}: non-finite output"
     assert np.array_equal(o_f, o_s), f"{what}: output differs from lm_rope + lm_attend_fp8"
     assert np.array_equal(kv_f, kv_s), f"{what}: FP8 cache differs"
@@ -245,10 +246,11 @@ def test_fused_fp8_equals_separate(heads, page, gh):
 
 def test_fused_fp8_config3_full_size_vs_oracle(oracle):
     """Config 3's shape over FP8 slots (128 rows, 32 heads, U[100, 3000], ring
-    3000): fused = separate bit for bit, and within tolerance of the oracle's
-    lm_rope + lm_attend_fp8 chain; the scatter's bytes equal the oracle's."""
+    3000) on the FP8 plan (768-key splits, 8 heads per workgroup): fused =
+    separate bit for bit, and within tolerance of the oracle's lm_rope +
+    lm_attend_fp8 chain; the scatter's bytes equal the oracle's."""
     c = W.fp8_ring_case(128, 32, 100, 3000, 3000, seed=3000, slack_pages=4)
-    o_f, kv_f, (slots, kv0) = check_identical_fp8(c, what="config 3 fp8")
+    o_f, kv_f, (slots, kv0) = check_identical_fp8(c, what="config 3 fp8", fp8_plan=True)
     q_want, kv_want = oracle.lm_rope(c.qkv, c.pos, slots, kv0, 32, COEF)
     want = oracle.lm_attend_fp8(q_want, kv_want, c.pos, c.seq, 0, c.indptr, c.pages, 16, 32, c.scale, 3000,
                                 nthreads=16)
