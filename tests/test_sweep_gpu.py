@@ -104,6 +104,16 @@ def test_prefill_sweep(oracle, case):
                         dev_i32(c.pages), page, out2, hq, hk, c.scale, plan, oa.workspace_for(plan))
         torch.cuda.synchronize()
         assert_close(host_bits(out2), want, what=f"{what} (decode kernel, chunk {plan.chunk})")
+    # The plan's exact_p on the same rows: within tolerance of the oracle, and
+    # (f32-P numerics) nearer to it on average than P rounded to bf16.
+    pf_x = oa.prefill_plan(c.rows, hq, hk, page, c.seq, c.pos, exact_p=True)
+    out3 = torch.zeros_like(out)
+    oa.prefill_run(pf_x, dev_bits(c.qkv), dev_bits(c.kv), dev_i32(c.pos), dev_i32(c.seq), dev_i32(c.indptr),
+                   dev_i32(c.pages), out3, c.scale)
+    torch.cuda.synchronize()
+    _, mean_x = assert_close(host_bits(out3), want, what=f"{what} (exact_p)")
+    _, mean_r = assert_close(host_bits(out), want, what=what)
+    assert mean_x <= mean_r * 1.05 + 1e-7, (what, mean_x, mean_r)
 
 
 @pytest.mark.parametrize("case", CASES)
