@@ -206,6 +206,22 @@ double prefill_step() {
   double worst = 0;
   check_close(dev_download<uint16_t>(out_p, out_o.size()), out_o, "prefill (MFMA)", &worst);
   check_close(dev_download<uint16_t>(out_d, out_o.size()), out_o, "prefill rows through decode", &worst);
+  // The same plan with exact_p set (P as two bf16 terms, the reference's f32-P
+  // numerics) on the rotated rows: within the tolerance too, and in bf16 bits
+  // the decode kernel's output on all but a few elements.
+  {
+    omni_attn_prefill_plan xplan = plan;
+    xplan.exact_p = 1;
+    OMNI_OK(omni_attn_prefill_run(&xplan, qkv, kv, pos, seq, indptr, pages, out_p, scale, work, st));
+    HIP_OK(hipStreamSynchronize(st));
+    const std::vector<uint16_t> got_x = dev_download<uint16_t>(out_p, out_o.size());
+    check_close(got_x, out_o, "prefill (MFMA, exact_p)", &worst);
+    const std::vector<uint16_t> got_d = dev_download<uint16_t>(out_d, out_o.size());
+    size_t same = 0;
+    for (size_t i = 0; i < got_x.size(); ++i) same += got_x[i] == got_d[i];
+    if (same * 100 < got_x.size() * 99) fail("exact_p prefill differs from the f32-P decode kernel on > 1% of elements");
+    std::printf("prefill exact_p: %.4f of elements equal the decode kernel's\n", (double)same / got_x.size());
+  }
   // V of every written slot is copied: bytes must match. K is rotated with
   // device math: within one bf16 ulp plus (2^-8 + pos * 2^-21) of its rotary
   // pair's magnitude (a last-bit difference in rsqrt or in the angle), and

@@ -4,7 +4,8 @@ attention) over the C ABI with no Python in the loop, captures the step once
 as a HIP graph and replays it for later steps, and checks every replay
 against an eager run (bit-identical) and the CPU oracle (to the tolerance).
 tests/c/engine_prefill.cpp does the same for a chunked ragged prefill (host
-prefill plan, MFMA prefill and decode on the same rows) and a HiDream step
+prefill plan, MFMA prefill with and without the plan's exact_p, and decode
+on the same rows) and a HiDream step
 (M-RoPE into the K/V caches, DiT attention replayed as a HIP graph with a
 changed key count)."""
 import os
