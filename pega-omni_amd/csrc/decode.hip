@@ -954,10 +954,13 @@ static int fp8_heads_per_group(const DecodeArgs& a, int rows) {
   return 1;
 }
 
-// Dynamic LDS the FP8 launch reserves and leaves unused: it holds the kernel
-// to two workgroups (eight waves) per CU where its 148 VGPRs would allow
-// three. Fewer reads in flight per CU read faster here: config 3 over FP8
-// slots 280.8-280.9 against 282.7-283.1 us per call (one box, alternating).
+// Dynamic LDS the FP8 launch reserves and leaves unused. With the kernel's
+// static LDS (8.25 KiB at 4 heads per workgroup, 16.25 KiB at 8) it holds the
+// launch to two workgroups per CU at 4 heads and to one at 8, where its
+// 142-148 VGPRs would allow three. Fewer reads in flight per CU read faster
+// here: config 3 over FP8 slots at 4 heads 280.8-280.9 against 282.7-283.1 us
+// per call with three per CU; at 8 heads (the FP8 plan's) 275.0-275.4 against
+// 280.4-281.0 with two per CU and 281.2-281.8 with three.
 constexpr int kFp8OccupancyLds = 64 << 10;
 
 template <int H, bool ROPE>
