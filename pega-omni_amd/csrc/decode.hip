@@ -963,6 +963,10 @@ static int fp8_heads_per_group(const DecodeArgs& a, int rows) {
 // 280.4-281.0 with two per CU and 281.2-281.8 with three.
 constexpr int kFp8OccupancyLds = 64 << 10;
 
+// Dynamic LDS that holds a head-group launch to one workgroup per CU (the
+// head-group launch below says when).
+constexpr int kMhSoloLds = 80 << 10;
+
 template <int H, bool ROPE>
 static void launch_fp8_hr(const DecodeArgs& a, int rows, hipStream_t stream) {
   const int units = rows * a.splits;
@@ -1038,16 +1042,27 @@ int launch_decode(const DecodeArgs& a, int rows, hipStream_t stream) {
   if (mh > 1) {
     const int H = mh;
     const dim3 g1((unsigned)(rows * (a.hk / H) * a.splits));
+    // One workgroup (four waves) per CU for large MHA launches of long splits:
+    // dynamic LDS the kernel does not use, beyond half the CU's 160 KiB with
+    // the kernel's static LDS, where its registers allow two. Fewer reads in
+    // flight per CU read faster there. lm_attend over bf16 slots (32 heads,
+    // lengths U[100, 3000], the plan's 1024-key splits, two heads per
+    // workgroup), us per call, one box, two alternations: 128 rows 483.0
+    // against 491.4-491.9, 256 rows 978 against 992-995, 512 rows 1868 against
+    // 1900. Shorter launches lose (16 rows on 256-key splits: 88 against
+    // 78 us; 32 rows on 512-key splits +1%), 64 rows on 1024-key splits
+    // (3072 workgroups) is even.
+    const int solo_lds = a.hq == a.hk && a.chunk >= 1024 && g1.x >= 4096 ? kMhSoloLds : 0;
 #define OMNI_MH(GG, HH)                                                                                  \
   {                                                                                                      \
     constexpr int kR = 4 / HH;                                                                           \
     const bool up = a.pd.page % kR == 0;                                                                 \
     if (div)                                                                                             \
-      up ? decode_split_mh<GG, HH, true, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows)               \
-         : decode_split_mh<GG, HH, false, true><<<g1, kDecodeThreads, 0, stream>>>(a, rows);             \
+      up ? decode_split_mh<GG, HH, true, true><<<g1, kDecodeThreads, solo_lds, stream>>>(a, rows)        \
+         : decode_split_mh<GG, HH, false, true><<<g1, kDecodeThreads, solo_lds, stream>>>(a, rows);      \
     else                                                                                                 \
-      up ? decode_split_mh<GG, HH, true, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows)              \
-         : decode_split_mh<GG, HH, false, false><<<g1, kDecodeThreads, 0, stream>>>(a, rows);            \
+      up ? decode_split_mh<GG, HH, true, false><<<g1, kDecodeThreads, solo_lds, stream>>>(a, rows)       \
+         : decode_split_mh<GG, HH, false, false><<<g1, kDecodeThreads, solo_lds, stream>>>(a, rows);     \
   }
     switch (a.hq / a.hk * 8 + H) {
       case 8 + 4: OMNI_MH(1, 4) break;
