@@ -63,12 +63,88 @@ __device__ __forceinline__ void row_angles(const RopeArgs& a, int n, int p, floa
   __syncthreads();
 }
 
+// The streaming path (STREAM below) with its first kRopePrefetch head loads
+// issued before the row's angle table is computed: their latency runs under
+// the sincos work and all of them are in flight at once, where the in-place q
+// stores would otherwise keep each head's load behind the previous head's
+// store. Measured on qwen3_rope over config 4's 25,499 prefill rows: 102.8-103.8
+// against 109.2-109.5 us per call (one box, alternating). The cached-load path keeps one head at a
+// time (with the same prefetch, hidream_qk_rope over config 5's rows took
+// 35.5-36.1 against 34.8-35.3 us).
+constexpr int kRopePrefetch = 4;
+
+template <int MODE>
+__device__ __forceinline__ void norm_rope_stream(const RopeArgs& a) {
+  const int n = blockIdx.x;
+  const int c = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int nh = a.hq + 2 * a.hk;
+  bf16_t* row = a.qkv + (int64_t)n * a.ld;
+  const int h0 = blockIdx.y * kHeadsPerGroup + grp, hstep = kHeadsPerGroup * gridDim.y;
+  uint4 pre[kRopePrefetch];
+#pragma unroll
+  for (int t = 0; t < kRopePrefetch; ++t)
+    if (h0 + t * hstep < nh) pre[t] = ldg16_stream(row + (int64_t)(h0 + t * hstep) * kHead + 8 * c);
+
+  int64_t slot;
+  int p = 0;
+  if constexpr (MODE == kDense) {
+    p = a.base + n % a.per;
+    slot = (int64_t)(n / a.per) * a.span + p;
+  } else {
+    slot = a.slots[n];
+    if constexpr (MODE == kPaged) p = a.pos[n];
+  }
+  __shared__ float s_cos[kHead / 2], s_sin[kHead / 2];
+  row_angles<MODE>(a, n, p, s_cos, s_sin);
+  float cs[8], sn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    cs[e] = s_cos[8 * (c & 7) + e];
+    sn[e] = s_sin[8 * (c & 7) + e];
+  }
+  float w[2][8];
+  widen8(ldg16(a.q_norm + 8 * c), w[0]);
+  widen8(ldg16(a.k_norm + 8 * c), w[1]);
+  const bool lo = c < 8;
+
+  auto head_out = [&](int head, const uint4& raw) {
+    if (head >= a.hq + a.hk) {  // V: a copy into the slot
+      bf16_t* dst = MODE == kMRope ? a.v_cache + (slot * a.hk + (head - a.hq - a.hk)) * kHead
+                                   : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead;
+      *reinterpret_cast<uint4*>(dst + 8 * c) = raw;
+      return;
+    }
+    float x[8];
+    widen8(raw, x);
+    const bool is_q = head < a.hq;
+    float ws[8], v[8], o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ws[e] = is_q ? w[0][e] : w[1][e];
+    rms_norm_head(x, ws, a.eps, v);
+    rotate_half(v, cs, sn, lo, o);
+    bf16_t* dst = is_q ? row + (int64_t)head * kHead
+                       : (MODE == kMRope ? a.k_cache + (slot * a.hk + (head - a.hq)) * kHead
+                                         : a.kv + (slot * 2 * a.hk + (head - a.hq)) * kHead);
+    *reinterpret_cast<uint4*>(dst + 8 * c) = pack8(o);
+  };
+  // Whole DPP rows take the same trip count.
+#pragma unroll
+  for (int t = 0; t < kRopePrefetch; ++t)
+    if (h0 + t * hstep < nh) head_out(h0 + t * hstep, pre[t]);
+  for (int head = h0 + kRopePrefetch * hstep; head < nh; head += hstep)
+    head_out(head, ldg16_stream(row + (int64_t)head * kHead + 8 * c));
+}
+
 // STREAM: the qkv rows are read with nontemporal loads. Worth it when they
 // exceed what the device's last-level cache would hold from the producing
 // kernel (measured: qwen3_rope over 313 MB of prefill rows -9%; over 107 MB
 // of DiT rows the cached loads are 16% faster).
 template <int MODE, bool STREAM>
 __global__ __launch_bounds__(kRopeThreads) void norm_rope(RopeArgs a) {
+  if constexpr (STREAM) {
+    norm_rope_stream<MODE>(a);
+    return;
+  }
   const int n = blockIdx.x;
   const int c = threadIdx.x & 15, grp = threadIdx.x >> 4;
 
